@@ -1,0 +1,170 @@
+"""ctypes access to the CPU oracle (oracle/liboracle.so) and, where it was built, the reference's own
+CPU conv path (oracle/_ref/libptref.so).  Test infrastructure: the checker, never the product."""
+from __future__ import annotations
+
+import ctypes as C
+import pathlib
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+ORACLE_SO = ROOT / "oracle" / "liboracle.so"
+REF_SO = ROOT / "oracle" / "_ref" / "libptref.so"
+
+F = C.POINTER(C.c_float)
+I64 = C.c_int64
+
+CONV_ARGS = [F, I64, I64, F, I64, I64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, F, F, I64,
+             C.c_int, C.c_int, C.c_float, C.c_float]
+CONVT_ARGS = [F, I64, I64, I64, F, I64, C.c_int, C.c_int, C.c_int, C.c_int, F, F, I64]
+
+
+def fptr(a: np.ndarray | None):
+    if a is None:
+        return F()
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(F)
+
+
+_oracle = None
+_ref = None
+
+
+def oracle():
+    global _oracle
+    if _oracle is None:
+        lib = C.CDLL(str(ORACLE_SO))
+        lib.orc_conv.argtypes = CONV_ARGS
+        lib.orc_convT.argtypes = CONVT_ARGS
+        lib.orc_epi.argtypes = [C.c_float, C.c_int, C.c_float]
+        lib.orc_epi.restype = C.c_float
+        lib.orc_decoder.argtypes = [C.c_void_p, F, I64, F, C.POINTER(F)]
+        lib.orc_mrf.argtypes = [C.POINTER(F), C.POINTER(F), C.c_int, I64, F, C.c_float, F]
+        lib.orc_tail.argtypes = [F, I64, F]
+        lib.orc_dec_constants.argtypes = [F, F, F, F]
+        lib.orc_dec_stage_len.argtypes = [C.c_int, I64]
+        lib.orc_dec_stage_len.restype = I64
+        lib.orc_set_conv_impl.argtypes = [C.c_void_p, C.c_void_p]
+        _oracle = lib
+    return _oracle
+
+
+def have_ref() -> bool:
+    return REF_SO.exists()
+
+
+def ref():
+    global _ref
+    if _ref is None:
+        lib = C.CDLL(str(REF_SO))
+        lib.ref_conv_cpu.argtypes = CONV_ARGS
+        lib.ref_convT_cpu.argtypes = CONVT_ARGS
+        lib.ref_ctx_layout.argtypes = [C.POINTER(C.c_long), C.c_int]
+        _ref = lib
+    return _ref
+
+
+def pad_rows(x: np.ndarray, pad: int) -> np.ndarray:
+    """The interpreter's zero-padded conv scratch (pt_v21_host.c:3274-3281)."""
+    *lead, T = x.shape
+    out = np.zeros((*lead, T + 2 * pad), np.float32)
+    out[..., pad:pad + T] = x
+    return np.ascontiguousarray(out)
+
+
+def conv(x, wp, bias, cout, K, stride=1, pad=0, dil=1, epi0=0, epi1=0, a0=0.0, a1=0.0, lib=None):
+    """CPU conv over unpadded x [batch][cin][T] -> [batch][cout4][Tout], via the oracle (or lib)."""
+    lib = lib or oracle()
+    fn = lib.orc_conv if hasattr(lib, "orc_conv") else lib.ref_conv_cpu
+    x = np.ascontiguousarray(x, np.float32)
+    if x.ndim == 2:
+        x = x[None]
+    batch, cin, T = x.shape
+    xp = pad_rows(x, pad)
+    Tout = (T + 2 * pad - (K - 1) * dil - 1) // stride + 1
+    c4 = (cout + 3) // 4 * 4
+    y = np.zeros((batch, c4, Tout), np.float32)
+    fn(fptr(xp), xp.shape[-1], cin, fptr(y), Tout, Tout, cout, K, stride, pad, dil,
+       fptr(np.ascontiguousarray(wp, np.float32)),
+       fptr(None if bias is None else np.ascontiguousarray(bias, np.float32)), batch, epi0, epi1,
+       a0, a1)
+    return y
+
+
+def convT(x, wp, bias, cout, K, s, pad, lib=None):
+    lib = lib or oracle()
+    fn = lib.orc_convT if hasattr(lib, "orc_convT") else lib.ref_convT_cpu
+    x = np.ascontiguousarray(x, np.float32)
+    if x.ndim == 2:
+        x = x[None]
+    batch, cin, tin = x.shape
+    Lout = (tin - 1) * s - 2 * pad + K
+    c4 = (cout + 3) // 4 * 4
+    y = np.zeros((batch, c4, Lout), np.float32)
+    fn(fptr(x), tin, cin, tin, fptr(y), Lout, cout, s, pad, K,
+       fptr(np.ascontiguousarray(wp, np.float32)),
+       fptr(None if bias is None else np.ascontiguousarray(bias, np.float32)), batch)
+    return y
+
+
+class DecWeights(C.Structure):
+    _fields_ = [("w", F * 40), ("b", F * 40)]
+
+
+def dec_weights_struct(ws, bs):
+    st = DecWeights()
+    for i in range(40):
+        st.w[i] = fptr(ws[i])
+        st.b[i] = fptr(bs[i])
+    return st
+
+
+def decoder(ws, bs, z, stages=False, use_ref=False):
+    lib = oracle()
+    if use_ref:
+        r = ref()
+        lib.orc_set_conv_impl(C.cast(r.ref_conv_cpu, C.c_void_p), C.cast(r.ref_convT_cpu, C.c_void_p))
+    try:
+        T = z.shape[-1]
+        wav = np.zeros(256 * T, np.float32)
+        st = dec_weights_struct(ws, bs)
+        bufs = None
+        sp = C.POINTER(F)()
+        if stages:
+            bufs = [np.zeros(lib.orc_dec_stage_len(i, T), np.float32) for i in range(6)]
+            arr = (F * 6)(*[fptr(b) for b in bufs])
+            sp = C.cast(arr, C.POINTER(F))
+        rc = lib.orc_decoder(C.byref(st), fptr(np.ascontiguousarray(z, np.float32)), T, fptr(wav), sp)
+        assert rc == 0
+    finally:
+        if use_ref:
+            lib.orc_set_conv_impl(None, None)
+    return (wav, bufs) if stages else wav
+
+
+def mrf(wts, bts, x, alpha):
+    lib = oracle()
+    C_, T = x.shape
+    out = np.zeros_like(x)
+    wa = (F * 18)(*[fptr(w) for w in wts])
+    ba = (F * 18)(*[fptr(b) for b in bts])
+    rc = lib.orc_mrf(wa, ba, C_, T, fptr(np.ascontiguousarray(x)), alpha, fptr(out))
+    assert rc == 0
+    return out
+
+
+def tail(p):
+    lib = oracle()
+    L = p.shape[-1]
+    wav = np.zeros(16 * (L - 1), np.float32)
+    assert lib.orc_tail(fptr(np.ascontiguousarray(p, np.float32)), L, fptr(wav)) == 0
+    return wav
+
+
+def constants():
+    hann = np.zeros(16, np.float32)
+    bc = np.zeros(144, np.float32)
+    bs = np.zeros(144, np.float32)
+    syn = np.zeros(4 * 63, np.float32)
+    oracle().orc_dec_constants(fptr(hann), fptr(bc), fptr(bs), fptr(syn))
+    return hann, bc.reshape(9, 16), bs.reshape(9, 16), syn.reshape(4, 63)
