@@ -1,0 +1,261 @@
+"""Benchmark of the MI355X conv hot path on BASELINE.json's metric:
+"conv TFLOP/s (% fp32-MFMA peak) + decoder audio-sec/sec at 1 and 8 streams".
+
+One step = BASELINE config 5, the largest single-GPU configuration: 8 independent decoder requests
+(T ~ U[56, 400] frames, seeded) on 8 contexts / HIP streams driven by 8 pthreads, plus one
+long-form request of T = 1500 frames through 96-frame overlap-save windows with 16-frame context
+on a ninth context, all sharing one uploaded weight set.  Inputs are resident in HBM before the
+timed region; `value` is the step's audio seconds divided by its wall time.  Alongside: config 4
+(one request, T = 226) on one stream, configs 1-3 in TFLOP/s, the dominant kernel against the
+fp32-MFMA roofline (HIP events on the stream it runs on), and the reference's CPU conv path timed
+on this host on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+       python bench.py --kernel-loop N   (only the dominant kernel, N launches: for rocprofv3 --pmc)
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import importlib.util
+import json
+import os
+import pathlib
+import sys
+import time
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent
+SR = 16000
+HOP = 256                      # output samples per frame
+MFMA_F32_PEAK = 157.3          # TFLOP/s, MI355X dense fp32 matrix (vendor figure)
+HBM_PEAK = 8000.0              # GB/s
+
+
+def _package():
+    init = ROOT / "prime-tts_amd" / "__init__.py"
+    spec = importlib.util.spec_from_file_location("prime_tts_amd", init,
+                                                  submodule_search_locations=[str(init.parent)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["prime_tts_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class EventTimer:
+    """HIP events recorded on a context's stream (the stream the kernels run on)."""
+
+    def __init__(self, pkg, ctx):
+        self.lib, self.ctx = pkg.load(), ctx
+        self.e0, self.e1 = self.lib.ptd_event_create(), self.lib.ptd_event_create()
+
+    def time(self, fn, reps):
+        self.lib.ptd_event_record(self.ctx.ptr, self.e0)
+        for _ in range(reps):
+            fn()
+        self.lib.ptd_event_record(self.ctx.ptr, self.e1)
+        ms = self.lib.ptd_event_elapsed_ms(self.e0, self.e1)
+        if ms < 0:
+            raise RuntimeError("event timing failed")
+        return ms / reps
+
+    def close(self):
+        self.lib.ptd_event_destroy(self.e0)
+        self.lib.ptd_event_destroy(self.e1)
+
+
+def mrf_depth_setup(pkg, ctx, stage, T):
+    C_ = 256 if stage == 0 else 128
+    rng = np.random.default_rng(77)
+    xs = [pkg.DevBuf.of(ctx, rng.standard_normal((C_, T)).astype(np.float32)) for _ in range(3)]
+    a_s = [pkg.DevBuf(C_ * T) for _ in range(3)]
+    ys = [pkg.DevBuf(C_ * T) for _ in range(3)]
+    arr = lambda bufs: (C.c_void_p * 3)(*[b.ptr for b in bufs])  # noqa: E731
+    return xs + a_s + ys, arr(xs), arr(a_s), arr(ys)
+
+
+def cpu_baseline(pkg):
+    """The reference's own CPU conv path (oracle/_ref, built from the reference sources) inside the
+    oracle's decoder driver, or the C restatement when _ref is absent: one config-4 request."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as ol
+    T = 226
+    ws, bs = pkg.synth.decoder_weights(1234)
+    z = pkg.synth.latent(T, 226)
+    kind = "reference" if ol.have_ref() else "port"
+    t0 = time.perf_counter()
+    ol.decoder(ws, bs, z, use_ref=kind == "reference")
+    dt = time.perf_counter() - t0
+    audio = T * HOP / SR
+    return {"value": round(audio / dt, 4), "unit": "audio-s/s", "cores": 1, "kind": kind,
+            "sample": f"one config-4 decode (T=226, {audio:.3f} s audio) on 1 host thread: {dt:.2f} s",
+            "model": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-loop", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the decoder path shards by request with no exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    pkg = _package()
+    lib = pkg.load()
+    ctx = pkg.Ctx(arena_mb=1024)
+    ws, bs = pkg.synth.decoder_weights(1234)
+    model = pkg.Model(ctx, ws, bs)
+    timer = EventTimer(pkg, ctx)
+
+    # ---------------------------------------------------------------- dominant kernel
+    # one MRF-256 depth at config 3 (C=256, T=904): two grouped conv launches of 3 branches each
+    flop_launch = 2.0 * 256 * 256 * 904 * (3 + 7 + 11)
+    bufs, xin, a_s, ys = mrf_depth_setup(pkg, ctx, 0, 904)
+    run_depth = lambda: lib.ptd_mrf_depth(ctx.ptr, model.ptr, 0, 2, xin, a_s, ys, 904)  # noqa: E731
+    if args.kernel_loop:
+        for _ in range(args.kernel_loop):
+            if run_depth() != 0:
+                raise RuntimeError("mrf depth failed")
+        ctx.sync()
+        log(f"kernel loop: {2 * args.kernel_loop} launches done")
+        return
+    for _ in range(5):
+        run_depth()
+    ms_depth = timer.time(run_depth, 50)
+    ms_launch = ms_depth / 2.0
+    achieved = flop_launch / (ms_launch * 1e-3) / 1e12
+    # algorithmic bytes of one launch (c1 group): 3 inputs + weights + biases + 3 outputs
+    bytes_launch = 4.0 * (3 * 256 * 904 + 256 * 256 * (3 + 7 + 11) + 3 * 256 + 3 * 256 * 904)
+    for b in bufs:
+        b.free()
+    log(f"dominant kernel: MRF-256 grouped conv {ms_launch * 1e3:.1f} us/launch = {achieved:.2f} TFLOP/s")
+
+    # ---------------------------------------------------------------- configs 1-3 (TFLOP/s)
+    cfg = {}
+    z226 = pkg.synth.latent(226, 226)
+    dz = pkg.DevBuf.of(ctx, z226)
+    dh = pkg.DevBuf(512 * 226)
+    f1 = lambda: lib.ptd_layer(ctx.ptr, model.ptr, 0, dz.ptr, 226, 1, dh.ptr, 0.0, 0.1)  # noqa: E731
+    f1()
+    ms = timer.time(f1, 50)
+    cfg["config1_conv_tflops"] = round(2 * 512 * 192 * 7 * 226 / (ms * 1e-3) / 1e12, 3)
+    dx0 = pkg.DevBuf(256 * 904)
+    f2 = lambda: lib.ptd_layer(ctx.ptr, model.ptr, 1, dh.ptr, 226, 1, dx0.ptr, 0.1, 0.0)  # noqa: E731
+    f2()
+    ms = timer.time(f2, 50)
+    cfg["config2_convT_tflops"] = round(2 * 256 * 512 * 4 * 904 / (ms * 1e-3) / 1e12, 3)
+    for stage, (C_, T) in enumerate([(256, 904), (128, 3616)]):
+        x = pkg.DevBuf.of(ctx, np.random.default_rng(5).standard_normal((C_, T)).astype(np.float32))
+        y = pkg.DevBuf(C_ * T)
+        f3 = lambda: lib.ptd_mrf(ctx.ptr, model.ptr, stage, x.ptr, T, 0.1, y.ptr)  # noqa: E731
+        f3()
+        ms = timer.time(f3, 20)
+        cfg[f"config3_mrf{C_}_tflops"] = round(2 * C_ * C_ * T * 3 * 21 / (ms * 1e-3) / 1e12, 3)
+        x.free()
+        y.free()
+    # config 4: one request, one stream
+    dw = pkg.DevBuf(HOP * 226)
+    f4 = lambda: lib.ptd_decode(ctx.ptr, model.ptr, dz.ptr, 226, 1, dw.ptr)  # noqa: E731
+    for _ in range(3):
+        f4()
+    ms4 = timer.time(f4, 20)
+    cfg["config4_ms_per_request"] = round(ms4, 4)
+    cfg["config4_audio_s_per_s_1stream"] = round(226 * HOP / SR / (ms4 * 1e-3), 2)
+    cfg["config4_decoder_tflops"] = round(32.571e9 / (ms4 * 1e-3) / 1e12, 3)
+    for b in (dz, dh, dx0, dw):
+        b.free()
+    log(f"configs: {cfg}")
+
+    # ---------------------------------------------------------------- config 5: the timed step
+    Ts = pkg.synth.request_lengths(5, 8)
+    T_long = 1500
+    zs = [pkg.DevBuf.of(ctx, pkg.synth.latent(T, 900 + i)) for i, T in enumerate(Ts + [T_long])]
+    wv = [pkg.DevBuf(HOP * T) for T in Ts + [T_long]]
+    reqs = [pkg.Request(zs[i].ptr, wv[i].ptr, T, 0, 0) for i, T in enumerate(Ts)]
+    reqs.append(pkg.Request(zs[-1].ptr, wv[-1].ptr, T_long, 96, 16))
+    req_arr = (pkg.Request * len(reqs))(*reqs)
+    arena = max(int(lib.ptd_decode_arena_bytes(max(Ts), 1)),
+                int(lib.ptd_windows_arena_bytes(T_long, 96, 16))) + (64 << 20)
+    srv = lib.ptd_server_create(len(reqs), arena)
+    if not srv:
+        raise RuntimeError("ptd_server_create failed")
+    wall = C.c_double()
+    for _ in range(args.warmup):
+        if lib.ptd_serve_run(srv, model.ptr, req_arr, len(reqs), C.byref(wall)) != 0:
+            raise RuntimeError("serve run failed")
+    lib.ptd_device_sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        if lib.ptd_serve_run(srv, model.ptr, req_arr, len(reqs), C.byref(wall)) != 0:
+            raise RuntimeError("serve run failed")
+    lib.ptd_device_sync()
+    dt = time.perf_counter() - t0
+    audio_step = sum(Ts + [T_long]) * HOP / SR
+    value = audio_step * args.steps / dt
+    audio8 = sum(Ts) * HOP / SR
+    lib.ptd_server_destroy(srv)
+    for b in zs + wv:
+        b.free()
+    log(f"config 5: {value:.1f} audio-s/s ({dt / args.steps * 1e3:.2f} ms/step)")
+
+    out = {
+        "metric": "decoder audio-sec/sec at 8 streams (+ conv TFLOP/s, % fp32-MFMA peak)",
+        "value": round(value, 2),
+        "unit": "audio-s/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded random-init decoder weights, N(0,1) latents)",
+        "config": {
+            "workload": "config 5: 8 concurrent MB-iSTFT decoder requests (T ~ U[56,400], seed 5) "
+                        "on 8 HIP streams + one T=1500 request in 96/16 overlap-save windows, "
+                        "one shared weight set",
+            "request_frames": Ts, "longform_frames": T_long, "audio_s_per_step": round(audio_step, 4),
+            "audio_s_8_requests": round(audio8, 4), "parallelism": "1 GPU, 9 streams",
+        },
+        "roofline": {
+            "kernel": "conv_mfma_kernel (MRF-256 grouped launch: 3 branch convs K 3/7/11, C 256, T 904)",
+            "bound": "mfma", "achieved": round(achieved, 3), "peak": MFMA_F32_PEAK,
+            "unit": "TFLOP/s", "frac": round(achieved / MFMA_F32_PEAK, 4),
+            "traffic": None,
+            "flop_per_launch": flop_launch, "alg_bytes_per_launch": bytes_launch,
+            "us_per_launch": round(ms_launch * 1e3, 3),
+        },
+        **cfg,
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline (reference conv path, 1 thread) ...")
+        out["cpu_baseline"] = cpu_baseline(pkg)
+    timer.close()
+    model.close()
+    ctx.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

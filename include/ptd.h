@@ -1,0 +1,124 @@
+/* ptd.h -- device-resident entry points of libptconv_hip.so, beside the reference ABI
+ * (pt_v21_dev.h).
+ *
+ * The reference ABI is synchronous and host-buffer based: every pt_v21_conv/convT call copies its
+ * input to the device and its output back unless a conv chain keeps it there.  These entry
+ * points keep a whole MB-iSTFT decoder request on the device, the reference's PT_V21_DEVADD idea
+ * (runtime/v21/src/pt_v21_host.c:2364-2543) carried through the decoder: every residual add,
+ * branch sum, /3 and LeakyReLU is fused into a conv's epilogue or input staging, and the iSTFT +
+ * PQMF tail is one kernel.  Same per-request model as the reference: one pt_ctx per request with
+ * its own stream and arena (pt_v21_cuda_init), one shared weight pool.
+ * All tensor pointers here are DEVICE pointers; calls only enqueue work on the context's stream
+ * unless the name says _host or sync. */
+#ifndef PTD_H_
+#define PTD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "pt_v21_dev.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Load n host records into the process-wide weight pool (one slab, 256-byte aligned records,
+ * claim-parallel upload on the caller's stream), the same pool pt_v21_cuda_init fills from a
+ * container.  Record i is then wtab/btab index i for pt_v21_conv/convT.  A pool that already
+ * holds records keeps them and returns 0 when n matches, -1 otherwise. */
+int ptd_pool_load(pt_ctx *c, int n, const void *const *host, const size_t *bytes);
+/* device pointer of pool record i, or NULL */
+const void *ptd_pool_record(int i);
+
+/* ---- synthetic MB-iSTFT decoder (ref/v21_graph_trace.txt:3819-4065) ------------------------ *
+ * 40 layers: 0 conv_pre, 1 ups.0, 2..19 MRF-256, 20 ups.1, 21..38 MRF-128, 39 conv_post; MRF
+ * order branch (K 3,7,11) x dilation (1,3,5) x (c1, c2).  Weights in the packed layouts. */
+#define PTD_DEC_NLAYER 40
+typedef struct ptd_model ptd_model;
+
+/* Uploads the 40 layers' weights and biases once into one device slab owned by the model and
+ * shared by every context, lays every weight out for the MFMA kernels and builds the tail's
+ * constant table.  Needs an initialised context (its stream does the upload).  NULL on failure. */
+ptd_model *ptd_model_create(pt_ctx *c, const float *const *w, const float *const *b);
+void ptd_model_destroy(ptd_model *m);
+
+/* Decode `batch` requests of T frames: z [batch][192][T] -> wav [batch][256*T].  Activations
+ * come from the context's arena (released on return); asynchronous on the context's stream.
+ * 0 / -1. */
+int ptd_decode(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int batch, float *wav);
+/* arena bytes one ptd_decode call needs */
+size_t ptd_decode_arena_bytes(int64_t T, int batch);
+/* Same, also copying the six stage tensors (conv_pre+leaky, ups.0, MRF-256 out, ups.1, MRF-128
+ * out, conv_post) of batch item 0 into the given device buffers (entries may be NULL). */
+int ptd_decode_stages(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, float *wav,
+                      float *const *stages);
+
+/* Run decoder layer i alone: conv (x [batch][cin][T] -> y [batch][cout4][Tout]) or convT
+ * (x [batch][cin][T] -> y [batch][cout4][Lout]).  in_leaky > 0 applies LeakyReLU(in_leaky) to
+ * the input as it is read; epi_leaky > 0 applies it to the output.  Asynchronous. */
+int ptd_layer(pt_ctx *c, const ptd_model *m, int layer, const float *x, int64_t T, int batch,
+              float *y, float in_leaky, float epi_leaky);
+/* One MRF stack (config 3): stage 0 = MRF-256 (layers 2..19), 1 = MRF-128 (21..38);
+ * x [C][T] -> out = leaky(((b0 + b1) + b2) / 3, alpha) [C][T].  Asynchronous. */
+int ptd_mrf(pt_ctx *c, const ptd_model *m, int stage, const float *x, int64_t T, float alpha,
+            float *out);
+
+/* One depth j (0..2, dilation 1/3/5) of an MRF stack: the three branches' c1 convs in one
+ * grouped launch (input xin[br] staged through LeakyReLU(0.1), epilogue LeakyReLU(0.1) -> a[br]),
+ * then their c2 convs in one grouped launch (epilogue adds the residual xin[br] -> y[br]).  All
+ * [C][T].  Asynchronous.  Two kernel launches of 2*C*C*T*(3+7+11) flops each. */
+int ptd_mrf_depth(pt_ctx *c, const ptd_model *m, int stage, int depth, const float *const *xin,
+                  float *const *a, float *const *y, int64_t T);
+
+/* Long-form request through overlap-save windows (config 5; the reference's streaming driver,
+ * main_v21_serve.c:210-264 with pt_v21_host.c:2749-2912): frames [a - ctx, a + hop + ctx) are
+ * decoded per window (clipped to the sequence) and the samples of frames [a, a + hop) are kept,
+ * hop = win - 2*ctx.  All windows are independent, so they run as one batched decode.
+ * z [192][T], wav [256*T].  Asynchronous. */
+int ptd_decode_windows(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int win, int ctx,
+                       float *wav);
+size_t ptd_windows_arena_bytes(int64_t T, int win, int ctx);
+
+/* ---- concurrent serving (config 5; the reference's main_v21_par.c:59-158 model) ------------ *
+ * nctx contexts (one stream + arena each, sharing the model's weights), each driven by its own
+ * pthread.  ptd_serve_run hands request r to context r % nctx, runs all requests, waits for
+ * all of them and returns the wall time in ms (host clock, from the first enqueue to the last
+ * stream's completion).  Requests with win > 0 use the windowed path. */
+typedef struct ptd_server ptd_server;
+ptd_server *ptd_server_create(int nctx, size_t arena_bytes);
+void ptd_server_destroy(ptd_server *s);
+pt_ctx *ptd_server_ctx(ptd_server *s, int i);
+typedef struct {
+  const float *z;   /* device [192][T] */
+  float *wav;       /* device [256*T] */
+  int64_t T;
+  int win, ctx;     /* win > 0: overlap-save windows */
+} ptd_request;
+int ptd_serve_run(ptd_server *s, const ptd_model *m, const ptd_request *req, int nreq,
+                  double *wall_ms);
+
+/* ---- plumbing for callers without a HIP runtime of their own (tests, bench.py) ------------ */
+void *ptd_malloc(size_t bytes);                 /* device memory, NULL on failure */
+void ptd_free(void *p);
+int ptd_h2d(pt_ctx *c, void *dst, const void *src, size_t bytes);   /* synchronous */
+int ptd_d2h(pt_ctx *c, void *dst, const void *src, size_t bytes);   /* synchronous */
+int ptd_sync(pt_ctx *c);                        /* wait for the context's stream */
+int ptd_device_sync(void);                      /* wait for every stream of the device */
+void *ptd_event_create(void);
+void ptd_event_destroy(void *e);
+int ptd_event_record(pt_ctx *c, void *e);       /* on the context's stream */
+float ptd_event_elapsed_ms(void *e0, void *e1); /* waits for e1; negative on error */
+
+/* fp32 32x32x2 MFMA lane-layout probe (test hook): d[32][32] = a[32][2] @ b[2][32], host
+ * buffers, synchronous on the context's stream. */
+int ptd_mfma_probe(pt_ctx *c, const float *a, const float *b, float *d);
+/* tail constant table as the device uses it (host copy, PTD_TAIL_NCONST floats) */
+#define PTD_TAIL_NCONST (16 + 144 + 144 + 252)
+void ptd_tail_constants(float *out);
+/* offsets of the pt_ctx fields the device layer touches (for the ABI test) */
+int ptd_ctx_layout(long *out, int n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

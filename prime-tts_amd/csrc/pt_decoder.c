@@ -1,0 +1,557 @@
+/* pt_decoder.c -- the synthetic MB-iSTFT decoder kept on the device, per request (C, gnu11).
+ *
+ * Graph (ref/v21_graph_trace.txt:3819-4065), with every host op of the reference fused:
+ *   conv_pre 192->512 K7 + LeakyReLU(0.1)          one conv, epilogue leaky
+ *   ups.0 convT 512->256 K16 s4 p6                  one phase-form GEMM (4 phases = 1024 rows)
+ *   MRF-256: per depth j, one grouped launch of the three branches' c1 (LeakyReLU(0.1) applied
+ *            to the input as it is staged, epilogue leaky), then one of their c2 (epilogue adds
+ *            the residual)  -> 6 launches, three branch outputs left in HBM
+ *   ups.1 convT 256->128: input staged as leaky(((b0 + b1) + b2) / 3, 0.1)
+ *   MRF-128 as above
+ *   conv_post 128->72 K7: input staged as leaky((...)/3, 0.01) through the (1, 0) reflection pad
+ *   tail: one kernel for exp/sin/cos -> irfft basis -> Hann -> OLA / window-sum -> [8:-8] ->
+ *         PQMF x4 zero-insert -> 63-tap FIR
+ * 17 launches per request, no host round trip.  The weights are uploaded once into one slab
+ * owned by the model and shared by every context; each context brings its own stream + arena. */
+#define _GNU_SOURCE
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "pt_dev_internal.h"
+#include "ptd.h"
+
+static const int kMrfK[3] = {3, 7, 11};
+static const int kMrfD[3] = {1, 3, 5};
+
+typedef struct {
+  int cin, cout, K, sd, pad, convT;
+} layer_geo;
+
+/* geometry of decoder layer i (spec/v21_layers.json, trace :3819-3935) */
+static layer_geo dec_geo(int i) {
+  layer_geo g = {0, 0, 0, 1, 0, 0};
+  if (i == 0) {
+    g.cin = 192; g.cout = 512; g.K = 7; g.pad = 3;
+  } else if (i == 1 || i == 20) {
+    g.cin = i == 1 ? 512 : 256; g.cout = i == 1 ? 256 : 128; g.K = 16; g.sd = 4; g.pad = 6; g.convT = 1;
+  } else if (i == 39) {
+    g.cin = 128; g.cout = 72; g.K = 7; g.pad = 3;
+  } else {
+    const int base = i < 20 ? 2 : 21, C = i < 20 ? 256 : 128, o = i - base;
+    const int br = o / 6, j = (o % 6) / 2, c = o % 2;
+    g.cin = C; g.cout = C; g.K = kMrfK[br];
+    g.sd = c == 0 ? kMrfD[j] : 1;
+    g.pad = g.sd * (g.K - 1) / 2;
+  }
+  return g;
+}
+
+struct ptd_model {
+  void *slab;                      /* relaid weights, biases, tail constants */
+  const float *wr[PTD_DEC_NLAYER]; /* MFMA layout [Mp/32][K][cinp][32] */
+  const float *b[PTD_DEC_NLAYER];
+  const float *consts;             /* hann, basis_c, basis_s, pqmf */
+  layer_geo g[PTD_DEC_NLAYER];
+};
+
+static size_t al256(size_t b) { return (b + 255) & ~(size_t) 255; }
+
+/* Constants of the tail (the same closed forms the reference graph folds into constants):
+ * periodic Hann(16); irfft basis rows w_k cos(2 pi k n / 16) / 16 and -w_k sin(...) / 16 with
+ * one-sided weights w = [1, 2, ..., 2, 1]; PQMF synthesis filters from the Kaiser-windowed sinc
+ * prototype (62 taps, cutoff 0.142, beta 9), cosine-modulated for 4 bands, gain 2. */
+void ptd_tail_constants(float *out) {
+  const double pi = 3.14159265358979323846;
+  float *hann = out, *bc = out + 16, *bs = out + 160, *h = out + 304;
+  for (int n = 0; n < 16; n++) hann[n] = (float) (0.5 - 0.5 * cos(2.0 * pi * n / 16.0));
+  for (int k = 0; k < 9; k++) {
+    const double w = (k == 0 || k == 8) ? 1.0 : 2.0;
+    for (int n = 0; n < 16; n++) {
+      bc[k * 16 + n] = (float) (w * cos(2.0 * pi * k * n / 16.0) / 16.0);
+      bs[k * 16 + n] = (float) (-w * sin(2.0 * pi * k * n / 16.0) / 16.0);
+    }
+  }
+  /* modified Bessel I0 by its power series (converges fast for the beta used here) */
+  double i0b = 1.0, term = 1.0;
+  for (int k = 1; k < 200; k++) {
+    term *= (81.0 / 4.0) / ((double) k * k);
+    i0b += term;
+    if (term < 1e-17 * i0b) break;
+  }
+  double proto[63];
+  for (int n = 0; n <= 62; n++) {
+    const double m = n - 31.0;
+    double v = n == 31 ? 0.142 : sin(pi * 0.142 * m) / (pi * m);
+    const double r = 2.0 * n / 62.0 - 1.0, x = 9.0 * sqrt(1.0 - r * r);
+    double i0 = 1.0, t = 1.0;
+    for (int k = 1; k < 200; k++) {
+      t *= (x * x / 4.0) / ((double) k * k);
+      i0 += t;
+      if (t < 1e-17 * i0) break;
+    }
+    proto[n] = v * i0 / i0b;
+  }
+  for (int k = 0; k < 4; k++) {
+    const double sg = (k & 1) ? -1.0 : 1.0;
+    for (int n = 0; n <= 62; n++)
+      h[k * 63 + n] = (float) (2.0 * proto[n] * cos((2 * k + 1) * (pi / 8.0) * (n - 31.0) - sg * pi / 4.0));
+  }
+}
+
+ptd_model *ptd_model_create(pt_ctx *c, const float *const *w, const float *const *b) {
+  if (!c || !c->use_cuda || !w || !b) return NULL;
+  ptd_model *m = calloc(1, sizeof *m);
+  if (!m) return NULL;
+  size_t total = 0, packed_max = 0;
+  size_t off_w[PTD_DEC_NLAYER], off_b[PTD_DEC_NLAYER], wbytes[PTD_DEC_NLAYER];
+  for (int i = 0; i < PTD_DEC_NLAYER; i++) {
+    layer_geo g = dec_geo(i);
+    m->g[i] = g;
+    const int c4 = (g.cout + 3) / 4 * 4;
+    const int M = g.convT ? g.sd * c4 : c4, K = g.convT ? (g.K + g.sd - 1) / g.sd : g.K;
+    wbytes[i] = (size_t) M * K * g.cin * sizeof(float);
+    if (wbytes[i] > packed_max) packed_max = wbytes[i];
+    off_w[i] = total;
+    total += al256(ptk_relayout_floats(M, K, g.cin) * sizeof(float));
+    off_b[i] = total;
+    total += al256((size_t) g.cout * sizeof(float));
+  }
+  const size_t off_c = total;
+  total += al256(PTD_TAIL_NCONST * sizeof(float));
+  float consts[PTD_TAIL_NCONST];
+  ptd_tail_constants(consts);
+  void *tmp = NULL;
+  if (ptk_malloc(&m->slab, total) || ptk_malloc(&tmp, packed_max)) goto fail;
+  char *base = (char *) m->slab;
+  for (int i = 0; i < PTD_DEC_NLAYER; i++) {
+    const layer_geo g = m->g[i];
+    const int c4 = (g.cout + 3) / 4 * 4;
+    const int M = g.convT ? g.sd * c4 : c4, K = g.convT ? (g.K + g.sd - 1) / g.sd : g.K;
+    /* the packed copy goes through one staging buffer; the stream orders reuse */
+    if (ptk_h2d_async(tmp, w[i], wbytes[i], c->g_stream) ||
+        ptk_relayout((float *) (base + off_w[i]), tmp, M, K, g.cin, c->g_stream) ||
+        ptk_h2d_async(base + off_b[i], b[i], (size_t) g.cout * sizeof(float), c->g_stream) ||
+        ptk_stream_sync(c->g_stream))
+      goto fail;
+    m->wr[i] = (const float *) (base + off_w[i]);
+    m->b[i] = (const float *) (base + off_b[i]);
+  }
+  if (ptk_h2d_async(base + off_c, consts, sizeof consts, c->g_stream) || ptk_stream_sync(c->g_stream))
+    goto fail;
+  m->consts = (const float *) (base + off_c);
+  ptk_free(tmp);
+  return m;
+fail:
+  PT_LOG("ptd_model_create failed: %s", ptk_last_error());
+  ptk_free(tmp);
+  ptk_free(m->slab);
+  free(m);
+  return NULL;
+}
+
+void ptd_model_destroy(ptd_model *m) {
+  if (!m) return;
+  ptk_device_sync();
+  ptk_free(m->slab);
+  free(m);
+}
+
+/* ------------------------------------------------------------------ building blocks */
+static void conv_layer_desc(ptk_conv_desc *d, const ptd_model *m, int i, const float *x,
+                            int64_t ldx, int64_t T, int batch, float *y, int64_t ldy) {
+  const layer_geo g = m->g[i];
+  const int c4 = (g.cout + 3) / 4 * 4;
+  ptdi_conv_desc(d, x, ldx, (int64_t) g.cin * ldx, T, g.cin, m->wr[i], m->b[i], g.cout, g.K, 1,
+                 g.sd, g.pad, c4, y, ldy, (int64_t) c4 * ldy, T, batch);
+}
+
+static void epi_push(ptk_conv_desc *d, int op, float a, const float *t, int64_t ldt, int64_t bst) {
+  d->epi[d->nepi].op = op;
+  d->epi[d->nepi].a = a;
+  d->epi[d->nepi].t = t;
+  d->epi[d->nepi].ldt = ldt;
+  d->epi[d->nepi].bst = bst;
+  d->nepi++;
+}
+
+/* one MRF depth for `batch` items: c1 group then c2 group (see ptd_mrf_depth) */
+static int mrf_depth(pt_ctx *c, const ptd_model *m, int stage, int j, const float *const *xin,
+                     float *const *a, float *const *y, int64_t T, int batch) {
+  const int base = stage == 0 ? 2 : 21, C = stage == 0 ? 256 : 128;
+  ptk_conv_desc d1[3], d2[3];
+  for (int br = 0; br < 3; br++) {
+    const int i1 = base + br * 6 + j * 2, i2 = i1 + 1;
+    conv_layer_desc(&d1[br], m, i1, xin[br], T, T, batch, a[br], T);
+    d1[br].in_op = PTK_IN_LEAKY;
+    d1[br].in_a = 0.1f;
+    epi_push(&d1[br], PTK_EPI_LEAKY, 0.1f, NULL, 0, 0);
+    conv_layer_desc(&d2[br], m, i2, a[br], T, T, batch, y[br], T);
+    epi_push(&d2[br], PTK_EPI_ADDT, 0.0f, xin[br], T, (int64_t) C * T);
+  }
+  if (ptk_conv_launch(d1, 3, c->g_stream) || ptk_conv_launch(d2, 3, c->g_stream)) {
+    PT_LOG("MRF depth %d failed: %s", j, ptk_last_error());
+    return -1;
+  }
+  return 0;
+}
+
+int ptd_mrf_depth(pt_ctx *c, const ptd_model *m, int stage, int depth, const float *const *xin,
+                  float *const *a, float *const *y, int64_t T) {
+  if (!c || !c->use_cuda || !m || (stage != 0 && stage != 1) || depth < 0 || depth > 2 || T < 1)
+    return -1;
+  return mrf_depth(c, m, stage, depth, xin, a, y, T, 1);
+}
+
+/* MRF stack on x [batch][C][T]: writes the three branch outputs (before the average) */
+static int mrf_run(pt_ctx *c, const ptd_model *m, int stage, const float *x, int64_t T, int batch,
+                   float *const out[3]) {
+  const int C = stage == 0 ? 256 : 128;
+  const size_t tb = (size_t) batch * C * T * sizeof(float);
+  float *a[3], *yb[3];
+  for (int br = 0; br < 3; br++) {
+    a[br] = ptdi_arena_alloc(c, tb);
+    yb[br] = ptdi_arena_alloc(c, tb);
+    if (!a[br] || !yb[br]) {
+      PT_LOG("arena too small for the MRF stack (T %lld batch %d)", (long long) T, batch);
+      return -1;
+    }
+  }
+  /* ping-pong: depth 0 writes out[], 1 writes yb[], 2 writes out[] again */
+  const float *prev[3] = {x, x, x};
+  for (int j = 0; j < 3; j++) {
+    float *cur[3];
+    for (int br = 0; br < 3; br++) cur[br] = (j == 1) ? yb[br] : out[br];
+    if (mrf_depth(c, m, stage, j, prev, a, cur, T, batch)) return -1;
+    for (int br = 0; br < 3; br++) prev[br] = cur[br];
+  }
+  return 0;
+}
+
+size_t ptd_decode_arena_bytes(int64_t T, int batch) {
+  const size_t f = sizeof(float) * (size_t) batch;
+  const int64_t T1 = 4 * T, T2 = 16 * T, L = T2 + 1;
+  size_t s = 0;
+  s += al256(f * 512 * T) + al256(f * 256 * T1) + 3 * al256(f * 256 * T1);   /* h, x0, o[] */
+  size_t mrf0 = 6 * al256(f * 256 * T1);
+  size_t late = al256(f * 128 * T2) + 3 * al256(f * 128 * T2) + 6 * al256(f * 128 * T2) + al256(f * 72 * L);
+  return s + (mrf0 > late ? mrf0 : late) + 4096;
+}
+
+static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int batch,
+                       float *wav, float *const *stages) {
+  if (!c || !c->use_cuda || !m || !z || !wav || T < 1 || batch < 1) return -1;
+  const int64_t T1 = 4 * T, T2 = 16 * T, L = T2 + 1;
+  const size_t f = sizeof(float) * (size_t) batch;
+  void *mark = ptdi_arena_mark(c);
+  int rc = -1;
+  float *h = ptdi_arena_alloc(c, f * 512 * T);
+  float *x0 = ptdi_arena_alloc(c, f * 256 * T1);
+  float *o0[3] = {ptdi_arena_alloc(c, f * 256 * T1), ptdi_arena_alloc(c, f * 256 * T1),
+                  ptdi_arena_alloc(c, f * 256 * T1)};
+  if (!h || !x0 || !o0[0] || !o0[1] || !o0[2]) goto oom;
+  ptk_conv_desc d;
+  /* conv_pre + LeakyReLU */
+  conv_layer_desc(&d, m, 0, z, T, T, batch, h, T);
+  epi_push(&d, PTK_EPI_LEAKY, 0.1f, NULL, 0, 0);
+  if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
+  /* ups.0 */
+  ptdi_convT_desc(&d, h, T, 512 * T, T, 512, m->wr[1], m->b[1], 256, 4, 6, 16, x0, T1, 256 * T1, batch);
+  if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
+  void *mark1 = ptdi_arena_mark(c);
+  if (mrf_run(c, m, 0, x0, T1, batch, o0)) goto fail;
+  ptdi_arena_release(c, mark1);   /* the MRF temporaries; o0[] stay */
+  float *x1 = ptdi_arena_alloc(c, f * 128 * T2);
+  float *o1[3] = {ptdi_arena_alloc(c, f * 128 * T2), ptdi_arena_alloc(c, f * 128 * T2),
+                  ptdi_arena_alloc(c, f * 128 * T2)};
+  if (!x1 || !o1[0] || !o1[1] || !o1[2]) goto oom;
+  /* ups.1 over leaky(avg(branches), 0.1) */
+  ptdi_convT_desc(&d, o0[0], T1, 256 * T1, T1, 256, m->wr[20], m->b[20], 128, 4, 6, 16, x1, T2,
+                  128 * T2, batch);
+  d.x1 = o0[1];
+  d.x2 = o0[2];
+  d.in_op = PTK_IN_AVG3_LEAKY;
+  d.in_a = 0.1f;
+  if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
+  void *mark2 = ptdi_arena_mark(c);
+  if (mrf_run(c, m, 1, x1, T2, batch, o1)) goto fail;
+  ptdi_arena_release(c, mark2);
+  float *p = ptdi_arena_alloc(c, f * 72 * L);
+  if (!p) goto oom;
+  /* conv_post over reflect_pad(1,0)(leaky(avg(branches), 0.01)) */
+  ptdi_conv_desc(&d, o1[0], T2, 128 * T2, L, 128, m->wr[39], m->b[39], 72, 7, 1, 1, 3, 72, p, L,
+                 72 * L, L, batch);
+  d.x1 = o1[1];
+  d.x2 = o1[2];
+  d.in_op = PTK_IN_AVG3_LEAKY;
+  d.in_a = 0.01f;
+  d.reflect_l1 = 1;
+  if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
+  if (ptk_tail_batched(p, L, 72 * L, L, wav, 256 * T, batch, m->consts, c->g_stream)) goto fail;
+  if (stages) {
+    const size_t fl = sizeof(float);
+    if ((stages[0] && ptk_d2d_async(stages[0], h, fl * 512 * T, c->g_stream)) ||
+        (stages[1] && ptk_d2d_async(stages[1], x0, fl * 256 * T1, c->g_stream)) ||
+        (stages[2] && ptk_avg3_leaky(o0[0], o0[1], o0[2], stages[2], 256 * T1, 0.1f, c->g_stream)) ||
+        (stages[3] && ptk_d2d_async(stages[3], x1, fl * 128 * T2, c->g_stream)) ||
+        (stages[4] && ptk_avg3_leaky(o1[0], o1[1], o1[2], stages[4], 128 * T2, 0.01f, c->g_stream)) ||
+        (stages[5] && ptk_d2d_async(stages[5], p, fl * 72 * L, c->g_stream)))
+      goto fail;
+  }
+  rc = 0;
+  goto done;
+oom:
+  PT_LOG("arena too small for a decode of T %lld x %d (need %zu MiB)", (long long) T, batch,
+         ptd_decode_arena_bytes(T, batch) >> 20);
+  goto done;
+fail:
+  PT_LOG("decode failed: %s", ptk_last_error());
+done:
+  ptdi_arena_release(c, mark);   /* later work on this stream is ordered after these kernels */
+  return rc;
+}
+
+int ptd_decode(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int batch, float *wav) {
+  return decode_impl(c, m, z, T, batch, wav, NULL);
+}
+
+int ptd_decode_stages(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, float *wav,
+                      float *const *stages) {
+  return decode_impl(c, m, z, T, 1, wav, stages);
+}
+
+int ptd_layer(pt_ctx *c, const ptd_model *m, int layer, const float *x, int64_t T, int batch,
+              float *y, float in_leaky, float epi_leaky) {
+  if (!c || !c->use_cuda || !m || layer < 0 || layer >= PTD_DEC_NLAYER || T < 1 || batch < 1) return -1;
+  const layer_geo g = m->g[layer];
+  ptk_conv_desc d;
+  if (g.convT) {
+    const int c4 = (g.cout + 3) / 4 * 4;
+    const int64_t Lout = (T - 1) * g.sd - 2 * g.pad + g.K;
+    ptdi_convT_desc(&d, x, T, (int64_t) g.cin * T, T, g.cin, m->wr[layer], m->b[layer], g.cout,
+                    g.sd, g.pad, g.K, y, Lout, (int64_t) c4 * Lout, batch);
+  } else {
+    conv_layer_desc(&d, m, layer, x, T, T, batch, y, T);
+  }
+  if (in_leaky > 0.0f) {
+    d.in_op = PTK_IN_LEAKY;
+    d.in_a = in_leaky;
+  }
+  if (epi_leaky > 0.0f) epi_push(&d, PTK_EPI_LEAKY, epi_leaky, NULL, 0, 0);
+  if (ptk_conv_launch(&d, 1, c->g_stream)) {
+    PT_LOG("ptd_layer %d failed: %s", layer, ptk_last_error());
+    return -1;
+  }
+  return 0;
+}
+
+int ptd_mrf(pt_ctx *c, const ptd_model *m, int stage, const float *x, int64_t T, float alpha,
+            float *out) {
+  if (!c || !c->use_cuda || !m || (stage != 0 && stage != 1) || T < 1) return -1;
+  const int C = stage == 0 ? 256 : 128;
+  const size_t tb = (size_t) C * T * sizeof(float);
+  void *mark = ptdi_arena_mark(c);
+  float *o[3] = {ptdi_arena_alloc(c, tb), ptdi_arena_alloc(c, tb), ptdi_arena_alloc(c, tb)};
+  int rc = -1;
+  if (o[0] && o[1] && o[2] && !mrf_run(c, m, stage, x, T, 1, o) &&
+      !ptk_avg3_leaky(o[0], o[1], o[2], out, (int64_t) C * T, alpha, c->g_stream))
+    rc = 0;
+  else
+    PT_LOG("ptd_mrf failed: %s", ptk_last_error());
+  ptdi_arena_release(c, mark);
+  return rc;
+}
+
+/* ------------------------------------------------------------------ overlap-save windows
+ * The reference's window schedule (main_v21_serve.c:229-257): window at frame a covers
+ * [a, a + min(win, T - a)); it emits [max(a + lo, emitted), min(a + hi, T)) with lo = ctx except
+ * for the first window, hi = width - ctx except for the last; the next window starts at
+ * emitted - ctx.  Windows of equal width run as one batched decode. */
+typedef struct {
+  int64_t a, w, e0, e1;
+} win_t;
+
+static int win_schedule(int64_t T, int win, int ctx, win_t *out, int cap) {
+  int n = 0;
+  int64_t a = 0, emitted = 0;
+  while (emitted < T && n < cap) {
+    int64_t w = win;
+    if (a + w > T) w = T - a;
+    const int last = a + w >= T;
+    const int64_t lo = a == 0 ? 0 : ctx, hi = last ? w : w - ctx;
+    int64_t e0 = a + lo, e1 = a + hi;
+    if (e0 < emitted) e0 = emitted;
+    if (e1 > T) e1 = T;
+    out[n].a = a;
+    out[n].w = w;
+    out[n].e0 = e0;
+    out[n].e1 = e1;
+    n++;
+    if (e1 > emitted) emitted = e1;
+    if (last) break;
+    a = e1 - ctx;
+    if (a <= 0) a = 1;
+  }
+  return n;
+}
+
+#define MAX_WIN 4096
+
+size_t ptd_windows_arena_bytes(int64_t T, int win, int ctx) {
+  win_t *w = malloc(sizeof(win_t) * MAX_WIN);
+  if (!w) return 0;
+  const int n = win_schedule(T, win, ctx, w, MAX_WIN);
+  int nfull = 0;
+  size_t tail = 0;
+  for (int i = 0; i < n; i++) {
+    if (w[i].w == win) nfull++;
+    else tail = ptd_decode_arena_bytes(w[i].w, 1) + al256(sizeof(float) * 256 * w[i].w) +
+                al256(sizeof(float) * 192 * w[i].w);
+  }
+  free(w);
+  size_t full = nfull ? ptd_decode_arena_bytes(win, nfull) + al256(sizeof(float) * nfull * 192 * win) +
+                            al256(sizeof(float) * nfull * 256 * win)
+                      : 0;
+  return full + tail + 4096;
+}
+
+int ptd_decode_windows(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int win, int ctx,
+                       float *wav) {
+  if (!c || !c->use_cuda || !m || T < 1 || win < 2 * ctx + 1 || ctx < 0) return -1;
+  win_t *ws = malloc(sizeof(win_t) * MAX_WIN);
+  if (!ws) return -1;
+  const int n = win_schedule(T, win, ctx, ws, MAX_WIN);
+  void *mark = ptdi_arena_mark(c);
+  int rc = -1, nfull = 0;
+  for (int i = 0; i < n; i++) nfull += ws[i].w == win;
+  const size_t fl = sizeof(float);
+  if (nfull) {
+    float *zb = ptdi_arena_alloc(c, fl * nfull * 192 * win);
+    float *wb = ptdi_arena_alloc(c, fl * nfull * 256 * win);
+    if (!zb || !wb) goto oom;
+    int k = 0;
+    for (int i = 0; i < n; i++) {
+      if (ws[i].w != win) continue;
+      if (ptk_d2d_2d_async(zb + (size_t) k * 192 * win, fl * win, z + ws[i].a, fl * T, fl * win, 192,
+                           c->g_stream))
+        goto fail;
+      k++;
+    }
+    if (decode_impl(c, m, zb, win, nfull, wb, NULL)) goto fail;
+    k = 0;
+    for (int i = 0; i < n; i++) {
+      if (ws[i].w != win) continue;
+      const int64_t cnt = (ws[i].e1 - ws[i].e0) * 256, skip = (ws[i].e0 - ws[i].a) * 256;
+      if (cnt > 0 && ptk_d2d_async(wav + ws[i].e0 * 256, wb + (size_t) k * 256 * win + skip,
+                                   fl * (size_t) cnt, c->g_stream))
+        goto fail;
+      k++;
+    }
+  }
+  for (int i = 0; i < n; i++) {
+    if (ws[i].w == win) continue;
+    const int64_t w = ws[i].w;
+    float *zb = ptdi_arena_alloc(c, fl * 192 * w), *wb = ptdi_arena_alloc(c, fl * 256 * w);
+    if (!zb || !wb) goto oom;
+    if (ptk_d2d_2d_async(zb, fl * w, z + ws[i].a, fl * T, fl * w, 192, c->g_stream) ||
+        decode_impl(c, m, zb, w, 1, wb, NULL))
+      goto fail;
+    const int64_t cnt = (ws[i].e1 - ws[i].e0) * 256, skip = (ws[i].e0 - ws[i].a) * 256;
+    if (cnt > 0 && ptk_d2d_async(wav + ws[i].e0 * 256, wb + skip, fl * (size_t) cnt, c->g_stream))
+      goto fail;
+  }
+  rc = 0;
+  goto done;
+oom:
+  PT_LOG("arena too small for windowed decode of T %lld (need %zu MiB)", (long long) T,
+         ptd_windows_arena_bytes(T, win, ctx) >> 20);
+  goto done;
+fail:
+  PT_LOG("windowed decode failed: %s", ptk_last_error());
+done:
+  ptdi_arena_release(c, mark);
+  free(ws);
+  return rc;
+}
+
+/* ------------------------------------------------------------------ concurrent serving */
+struct ptd_server {
+  int n;
+  pt_ctx *ctx;
+};
+
+ptd_server *ptd_server_create(int nctx, size_t arena_bytes) {
+  if (nctx < 1) return NULL;
+  ptd_server *s = calloc(1, sizeof *s);
+  if (!s) return NULL;
+  s->ctx = calloc((size_t) nctx, sizeof(pt_ctx));
+  if (!s->ctx) {
+    free(s);
+    return NULL;
+  }
+  for (int i = 0; i < nctx; i++) {
+    if (ptdi_ctx_init(&s->ctx[i], arena_bytes, 0)) {
+      s->n = i;
+      ptd_server_destroy(s);
+      return NULL;
+    }
+  }
+  s->n = nctx;
+  return s;
+}
+
+void ptd_server_destroy(ptd_server *s) {
+  if (!s) return;
+  for (int i = 0; i < s->n; i++) pt_v21_cuda_shutdown(&s->ctx[i]);
+  free(s->ctx);
+  free(s);
+}
+
+pt_ctx *ptd_server_ctx(ptd_server *s, int i) {
+  return (s && i >= 0 && i < s->n) ? &s->ctx[i] : NULL;
+}
+
+typedef struct {
+  pt_ctx *c;
+  const ptd_model *m;
+  const ptd_request *req;
+  int nreq, first, step, rc;
+} worker_arg;
+
+static void *worker(void *p) {
+  worker_arg *a = (worker_arg *) p;
+  pt_v21_cuda_active(1);
+  a->rc = 0;
+  for (int r = a->first; r < a->nreq && !a->rc; r += a->step) {
+    const ptd_request *q = &a->req[r];
+    a->rc = q->win > 0 ? ptd_decode_windows(a->c, a->m, q->z, q->T, q->win, q->ctx, q->wav)
+                       : ptd_decode(a->c, a->m, q->z, q->T, 1, q->wav);
+  }
+  if (ptdi_wait(a->c)) a->rc = -1;
+  pt_v21_cuda_active(-1);
+  return NULL;
+}
+
+int ptd_serve_run(ptd_server *s, const ptd_model *m, const ptd_request *req, int nreq,
+                  double *wall_ms) {
+  if (!s || !m || !req || nreq < 1) return -1;
+  const int nt = s->n < nreq ? s->n : nreq;
+  pthread_t th[256];
+  worker_arg args[256];
+  if (nt > 256) return -1;
+  const double t0 = ptdi_now_ms();
+  int started = 0;
+  for (int i = 0; i < nt; i++) {
+    args[i] = (worker_arg){&s->ctx[i], m, req, nreq, i, s->n, 0};
+    if (pthread_create(&th[i], NULL, worker, &args[i])) break;
+    started++;
+  }
+  int rc = started == nt ? 0 : -1;
+  for (int i = 0; i < started; i++) {
+    pthread_join(th[i], NULL);
+    if (args[i].rc) rc = -1;
+  }
+  if (wall_ms) *wall_ms = ptdi_now_ms() - t0;
+  return rc;
+}

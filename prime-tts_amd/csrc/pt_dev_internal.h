@@ -1,0 +1,50 @@
+/* pt_dev_internal.h -- shared between the C host files of libptconv_hip.so (not installed). */
+#ifndef PT_DEV_INTERNAL_H_
+#define PT_DEV_INTERNAL_H_
+
+#include <stddef.h>
+#include <stdio.h>
+
+#include "pt_v21_dev.h"
+#include "ptk.h"
+
+#define PT_LOG(...)                     \
+  do {                                  \
+    fprintf(stderr, "pt_v21 hip: ");    \
+    fprintf(stderr, __VA_ARGS__);       \
+    fputc('\n', stderr);                \
+  } while (0)
+
+/* arena: per-context bump allocator, 256-byte aligned, mark / release */
+void *ptdi_arena_alloc(pt_ctx *c, size_t bytes);
+void *ptdi_arena_mark(pt_ctx *c);
+void ptdi_arena_release(pt_ctx *c, void *mark);
+
+/* weight pool: device pointer of record idx when it holds at least `need` bytes, else NULL */
+const void *ptdi_pool_get(int idx, size_t need);
+/* relaid MFMA copy of pool record idx for (M rows, K taps, cin), built once per process on the
+ * caller's stream; NULL when idx is not resident */
+const float *ptdi_pool_relaid(pt_ctx *c, int idx, int M, int K, int cin);
+/* take / drop a reference on the pool (init / shutdown) */
+void ptdi_pool_ref(int delta);
+
+/* wait for the context's stream under the wait policy (PT_V21_WAIT_US); 0 / -1 */
+int ptdi_wait(pt_ctx *c);
+
+/* fill a conv descriptor for a plain conv over device buffers (in_op / epilogues left empty) */
+void ptdi_conv_desc(ptk_conv_desc *d, const float *x, int64_t ldx, int64_t bsx, int64_t lim,
+                    int cin, const float *wr, const float *bias, int nbias, int K, int stride,
+                    int dil, int shift, int M, float *y, int64_t ldy, int64_t bsy, int64_t n,
+                    int batch);
+/* same for a convT in the phase form; returns the output length */
+int64_t ptdi_convT_desc(ptk_conv_desc *d, const float *x, int64_t ldx, int64_t bsx, int64_t tin,
+                        int cin, const float *wr, const float *bias, int cout, int s, int pad,
+                        int K, float *y, int64_t ldy, int64_t bsy, int batch);
+
+/* pt_v21_cuda_init with an explicit arena size */
+int ptdi_ctx_init(pt_ctx *c, size_t arena_bytes, int verbose);
+
+/* elapsed wall-clock ms since an arbitrary origin */
+double ptdi_now_ms(void);
+
+#endif

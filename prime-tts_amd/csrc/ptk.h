@@ -1,0 +1,148 @@
+/* ptk.h -- the thin C-ABI layer between the C (gnu11) host code and the HIP side.
+ *
+ * Everything HIP lives behind these functions (ptk_kernels.hip): stream and memory wrappers, the
+ * one-time weight relayout, and the conv / convT / elementwise / decoder-tail launchers.  The
+ * host code never includes a HIP header.  All sizes are elements unless named *_bytes; every
+ * pointer handed to a launcher is a device pointer.  Launchers only enqueue work on the given
+ * stream; they return 0, or -1 with the reason in ptk_last_error(). */
+#ifndef PTK_H_
+#define PTK_H_
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- runtime wrappers */
+int ptk_init(void);                                /* select device 0 once; 0 / -1 */
+const char *ptk_last_error(void);
+int ptk_stream_create(void **s);                   /* non-blocking stream, default priority */
+int ptk_stream_destroy(void *s);
+int ptk_stream_sync(void *s);
+int ptk_stream_query(void *s);                     /* 1 done, 0 busy, -1 error */
+int ptk_malloc(void **p, size_t bytes);
+int ptk_free(void *p);
+int ptk_h2d_async(void *dst, const void *src, size_t bytes, void *s);
+int ptk_d2h_async(void *dst, const void *src, size_t bytes, void *s);
+int ptk_d2d_async(void *dst, const void *src, size_t bytes, void *s);
+/* row-strided copies: height rows of width_bytes, pitches in bytes */
+int ptk_d2d_2d_async(void *dst, size_t dpitch, const void *src, size_t spitch, size_t width_bytes,
+                     size_t height, void *s);
+int ptk_d2h_2d_async(void *dst, size_t dpitch, const void *src, size_t spitch, size_t width_bytes,
+                     size_t height, void *s);
+int ptk_h2d_2d_async(void *dst, size_t dpitch, const void *src, size_t spitch, size_t width_bytes,
+                     size_t height, void *s);
+int ptk_event_create(void **e);
+int ptk_event_destroy(void *e);
+int ptk_event_record(void *e, void *s);
+int ptk_stream_wait_event(void *s, void *e);
+int ptk_event_elapsed_ms(float *ms, void *e0, void *e1);
+int ptk_event_sync(void *e);
+int ptk_device_sync(void);
+
+/* ---------------------------------------------------------------- conv problem descriptor
+ * One implicit-GEMM problem.  Row m of the GEMM is an output channel (conv: m = co) or a phase
+ * row (convT: m = r*C4 + co); column q is an output position of that row.  Reduction index
+ * (k, ci): tap k, input channel ci.  Input column read for (q, k):
+ *     c = q*stride + k*dil - shift          (convT phase form: stride 1, dil -1, shift 0)
+ * c outside [0, lim) reads 0 (in-kernel zero padding and the convT tail flush).
+ * Output for row m = r*C4 + co and column q goes to  y[b*bsy + co*ldy + (q*ys + r - ypad)]
+ * when that index is in [0, Lout) (conv: C4 = M, ys = 1, ypad = 0). */
+enum { PTK_IN_PLAIN = 0, PTK_IN_LEAKY = 1, PTK_IN_AVG3_LEAKY = 2 };
+enum {
+  PTK_EPI_NONE = 0,
+  PTK_EPI_LEAKY = 1,   /* v >= 0 ? v : a*v                        (reference op code 1) */
+  PTK_EPI_RELU = 2,    /* v > 0 ? v : 0                            (reference op code 2) */
+  PTK_EPI_MULS = 3,    /* v * a                                    (reference op code 3) */
+  PTK_EPI_ADDS = 4,    /* v + a                                    (reference op code 4) */
+  PTK_EPI_ADDT = 5,    /* v + t[b*bst + co*ldt + col]  (residual / branch sum; same layout as y) */
+  PTK_EPI_DIVS = 6     /* v / a                                                                  */
+};
+#define PTK_MAX_EPI 4
+#define PTK_MAX_GROUP 4
+
+typedef struct {
+  int op;
+  float a;
+  const float *t;
+  int64_t ldt, bst;
+} ptk_epi;
+
+typedef struct {
+  /* input */
+  const float *x, *x1, *x2;   /* x1, x2 only for PTK_IN_AVG3_LEAKY */
+  int64_t ldx, bsx;           /* row stride, batch stride (elements) */
+  int64_t lim;                /* valid virtual input columns [0, lim) */
+  int cin;
+  int in_op;
+  float in_a;
+  int reflect_l1;             /* virtual column 0 reads physical column 1, column c>0 reads c-1 */
+  /* weights: relaid [Mp/32][K][cinp][32] (see ptk_relayout) */
+  const float *w;
+  int cinp;
+  const float *bias;
+  int nbias;
+  int K, dil, stride, shift;
+  int M;                      /* GEMM rows (cout4 or s*cout4) */
+  int C4;                     /* rows per phase (conv: M) */
+  int64_t q0, nq;             /* output columns [q0, q0 + nq) */
+  /* output */
+  float *y;
+  int64_t ldy, bsy;
+  int ys, ypad;
+  int64_t Lout;
+  int batch;
+  int nepi;
+  ptk_epi epi[PTK_MAX_EPI];
+} ptk_conv_desc;
+
+/* Relayout packed conv/convT weights [M/4][K][cin][4] into the MFMA operand layout
+ * [Mp/32][K][cinp][32] (Mp = M rounded up to 32, zero rows/channels in the padding).  Returns the
+ * cinp the kernels expect for this cin (ptk_conv_cinp). */
+int ptk_conv_cinp(int cin);
+size_t ptk_relayout_floats(int M, int K, int cin);
+int ptk_relayout(float *dst, const float *wp, int M, int K, int cin, void *s);
+
+/* Launch ngroup independent problems (1..PTK_MAX_GROUP) in one grid; heavy problems first.
+ * Returns 0, or -1 when a shape is outside what the kernels support (ptk_last_error says why). */
+int ptk_conv_launch(const ptk_conv_desc *d, int ngroup, void *s);
+/* 1 when the MFMA kernel covers this problem's shape; else the caller uses the SIMT path */
+int ptk_conv_mfma_ok(const ptk_conv_desc *d);
+
+/* SIMT fallbacks over the PACKED layouts, for narrow shapes (cout4 < 16, tiny cin, huge K*dil):
+ * conv: X rows of ldx with in-kernel padding by `shift`; convT: the phase/tap form. */
+int ptk_conv_simt(const float *x, int64_t ldx, int64_t bsx, int64_t lim, int cin, const float *wp,
+                  const float *bias, int cout, int K, int stride, int dil, int shift, float *y,
+                  int64_t ldy, int64_t bsy, int64_t n, int batch, int epi0, float a0, int epi1,
+                  float a1, void *s);
+int ptk_convT_simt(const float *x, int64_t ldx, int64_t bsx, int64_t tin, int cin,
+                   const float *wp, const float *bias, int cout, int st, int pad, int K, float *y,
+                   int64_t ldy, int64_t bsy, int64_t Lout, int batch, void *s);
+
+/* C[m][nn] = A[m][k] @ B[k][nn], row strides lda/ldb/ldc; one thread per output, p ascending */
+int ptk_matmul(const float *A, int64_t m, int64_t k, int64_t lda, const float *B, int64_t ldb,
+               int64_t nn, float *C, int64_t ldc, void *s);
+
+/* elementwise: y = a + b (+ leaky when epi == 1), y = leaky(a) -- fp32, same ops as the host */
+int ptk_add(const float *a, const float *b, float *y, int64_t n, int epi, float alpha, void *s);
+int ptk_leaky(const float *a, float *y, int64_t n, float alpha, void *s);
+/* y = leaky(((a + b) + c) / 3, alpha): the MRF branch average (ref/v21_graph_trace.txt:3851-3869) */
+int ptk_avg3_leaky(const float *a, const float *b, const float *c, float *y, int64_t n, float alpha,
+                   void *s);
+
+/* decoder tail: conv_post output p [72][L] (row stride ldp) -> wav [16*(L-1)] (iSTFT + PQMF) */
+int ptk_tail(const float *p, int64_t ldp, int64_t L, float *wav, const float *consts, void *s);
+/* batched: item b reads p + b*bsp and writes wav + b*bsw */
+int ptk_tail_batched(const float *p, int64_t ldp, int64_t bsp, int64_t L, float *wav, int64_t bsw,
+                     int batch, const float *consts, void *s);
+/* the tail's constant table (floats): hann[16], basis_c[9*16], basis_s[9*16], pqmf[4*63] */
+#define PTK_TAIL_NCONST (16 + 144 + 144 + 252)
+
+/* lane-layout probe of the fp32 32x32x2 MFMA builtin: d[32][32] = a[32][2] @ b[2][32] */
+int ptk_mfma_probe(const float *a, const float *b, float *d, void *s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

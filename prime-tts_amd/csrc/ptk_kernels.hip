@@ -1,0 +1,746 @@
+// ptk_kernels.hip -- gfx950 (MI355X) kernels of the PrimeTTS conv hot path, and the thin C-ABI
+// layer (ptk.h) through which the C host code reaches them.
+//
+// Wide Conv1d / ConvTranspose1d run as one implicit GEMM on the fp32 matrix cores
+// (v_mfma_f32_32x32x2_f32): GEMM rows are output channels (convT: phase rows r*C4 + co, the
+// reference's packed phase layout), columns are output positions, the reduction runs over
+// (tap, input channel).  im2col never exists: each wave stages a window of input columns per
+// channel chunk in LDS and reads it K times at the K tap shifts.  The four waves of a workgroup
+// split the input channels and reduce through LDS in a fixed order (deterministic), then the
+// epilogue (bias, LeakyReLU/ReLU/scalar ops, residual / branch-sum tensor adds, division) is
+// applied on the accumulator values right before the single store.
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "ptk.h"
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// ------------------------------------------------------------------------------ error handling
+static thread_local char g_err[512];
+
+static void set_err(const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+}
+
+#define HCHK(x)                                                                  \
+  do {                                                                           \
+    hipError_t e_ = (x);                                                         \
+    if (e_ != hipSuccess) {                                                      \
+      set_err("%s failed: %s (%s:%d)", #x, hipGetErrorString(e_), __FILE__, __LINE__); \
+      return -1;                                                                 \
+    }                                                                            \
+  } while (0)
+
+extern "C" const char *ptk_last_error(void) { return g_err; }
+
+// ------------------------------------------------------------------------------ runtime wrappers
+extern "C" int ptk_init(void) {
+  static int done = 0;
+  if (done) return 0;
+  int n = 0;
+  HCHK(hipGetDeviceCount(&n));
+  if (n < 1) {
+    set_err("no HIP device");
+    return -1;
+  }
+  HCHK(hipSetDevice(0));
+  done = 1;
+  return 0;
+}
+extern "C" int ptk_stream_create(void **s) {
+  hipStream_t st;
+  HCHK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+  *s = (void *) st;
+  return 0;
+}
+extern "C" int ptk_stream_destroy(void *s) {
+  HCHK(hipStreamDestroy((hipStream_t) s));
+  return 0;
+}
+extern "C" int ptk_stream_sync(void *s) {
+  HCHK(hipStreamSynchronize((hipStream_t) s));
+  return 0;
+}
+extern "C" int ptk_stream_query(void *s) {
+  hipError_t e = hipStreamQuery((hipStream_t) s);
+  if (e == hipSuccess) return 1;
+  if (e == hipErrorNotReady) return 0;
+  set_err("hipStreamQuery: %s", hipGetErrorString(e));
+  return -1;
+}
+extern "C" int ptk_malloc(void **p, size_t bytes) {
+  HCHK(hipMalloc(p, bytes ? bytes : 1));
+  return 0;
+}
+extern "C" int ptk_free(void *p) {
+  if (p) HCHK(hipFree(p));
+  return 0;
+}
+extern "C" int ptk_h2d_async(void *dst, const void *src, size_t bytes, void *s) {
+  if (bytes) HCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t) s));
+  return 0;
+}
+extern "C" int ptk_d2h_async(void *dst, const void *src, size_t bytes, void *s) {
+  if (bytes) HCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t) s));
+  return 0;
+}
+extern "C" int ptk_d2d_async(void *dst, const void *src, size_t bytes, void *s) {
+  if (bytes) HCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t) s));
+  return 0;
+}
+extern "C" int ptk_d2d_2d_async(void *dst, size_t dpitch, const void *src, size_t spitch,
+                                size_t wb, size_t h, void *s) {
+  if (wb && h)
+    HCHK(hipMemcpy2DAsync(dst, dpitch, src, spitch, wb, h, hipMemcpyDeviceToDevice, (hipStream_t) s));
+  return 0;
+}
+extern "C" int ptk_d2h_2d_async(void *dst, size_t dpitch, const void *src, size_t spitch,
+                                size_t wb, size_t h, void *s) {
+  if (wb && h)
+    HCHK(hipMemcpy2DAsync(dst, dpitch, src, spitch, wb, h, hipMemcpyDeviceToHost, (hipStream_t) s));
+  return 0;
+}
+extern "C" int ptk_h2d_2d_async(void *dst, size_t dpitch, const void *src, size_t spitch,
+                                size_t wb, size_t h, void *s) {
+  if (wb && h)
+    HCHK(hipMemcpy2DAsync(dst, dpitch, src, spitch, wb, h, hipMemcpyHostToDevice, (hipStream_t) s));
+  return 0;
+}
+extern "C" int ptk_event_create(void **e) {
+  hipEvent_t ev;
+  HCHK(hipEventCreate(&ev));
+  *e = (void *) ev;
+  return 0;
+}
+extern "C" int ptk_event_destroy(void *e) {
+  HCHK(hipEventDestroy((hipEvent_t) e));
+  return 0;
+}
+extern "C" int ptk_event_record(void *e, void *s) {
+  HCHK(hipEventRecord((hipEvent_t) e, (hipStream_t) s));
+  return 0;
+}
+extern "C" int ptk_stream_wait_event(void *s, void *e) {
+  HCHK(hipStreamWaitEvent((hipStream_t) s, (hipEvent_t) e, 0));
+  return 0;
+}
+extern "C" int ptk_event_elapsed_ms(float *ms, void *e0, void *e1) {
+  HCHK(hipEventElapsedTime(ms, (hipEvent_t) e0, (hipEvent_t) e1));
+  return 0;
+}
+extern "C" int ptk_event_sync(void *e) {
+  HCHK(hipEventSynchronize((hipEvent_t) e));
+  return 0;
+}
+extern "C" int ptk_device_sync(void) {
+  HCHK(hipDeviceSynchronize());
+  return 0;
+}
+
+// ------------------------------------------------------------------------------ weight relayout
+// Packed [M/4][K][cin][4] (the reference's conv layout; a convT's phase rows are just more rows)
+// -> MFMA operand layout [Mp/32][K][cinp][32]: for a fixed (row block, tap, channel) the 32 rows
+// are contiguous, so the A operand of a 32x32x2 MFMA (32 rows x 2 channels) is two 128-byte
+// segments.  cinp rounds cin up so every wave of the 4-way channel split owns whole chunks.
+#define CONV_CK 8          // input channels per staged chunk (per wave)
+#define CONV_WAVES 4       // waves per workgroup, each owning a quarter of the channels
+#define CONV_XWMAX 192     // widest input window (columns) a wave stages per channel
+
+extern "C" int ptk_conv_cinp(int cin) {
+  const int q = CONV_WAVES * CONV_CK;
+  return (cin + q - 1) / q * q;
+}
+extern "C" size_t ptk_relayout_floats(int M, int K, int cin) {
+  const size_t Mp = (size_t) (M + 31) / 32 * 32;
+  return Mp * (size_t) K * (size_t) ptk_conv_cinp(cin);
+}
+
+__global__ void relayout_kernel(float *__restrict__ dst, const float *__restrict__ wp, int M,
+                                int K, int cin, int cinp, long long total) {
+  long long i = (long long) blockIdx.x * blockDim.x + threadIdx.x;
+  const long long st = (long long) gridDim.x * blockDim.x;
+  for (; i < total; i += st) {
+    const int mm = (int) (i & 31);
+    long long r = i >> 5;
+    const int ci = (int) (r % cinp);
+    r /= cinp;
+    const int k = (int) (r % K);
+    const int mb = (int) (r / K);
+    const int m = mb * 32 + mm;
+    float v = 0.0f;
+    if (m < M && ci < cin) v = wp[(((long long) (m >> 2) * K + k) * cin + ci) * 4 + (m & 3)];
+    dst[i] = v;
+  }
+}
+
+extern "C" int ptk_relayout(float *dst, const float *wp, int M, int K, int cin, void *s) {
+  const long long total = (long long) ptk_relayout_floats(M, K, cin);
+  long long blocks = (total + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(relayout_kernel, dim3((unsigned) blocks), dim3(256), 0, (hipStream_t) s, dst,
+                     wp, M, K, cin, ptk_conv_cinp(cin), total);
+  HCHK(hipGetLastError());
+  return 0;
+}
+
+// ------------------------------------------------------------------------------ epilogue
+__device__ __forceinline__ float epi_apply(float v, const ptk_epi &e, int b, int co, long long col) {
+  switch (e.op) {
+    case PTK_EPI_LEAKY: return v >= 0.0f ? v : e.a * v;
+    case PTK_EPI_RELU: return v > 0.0f ? v : 0.0f;
+    case PTK_EPI_MULS: return v * e.a;
+    case PTK_EPI_ADDS: return v + e.a;
+    case PTK_EPI_ADDT: return v + e.t[(long long) b * e.bst + (long long) co * e.ldt + col];
+    case PTK_EPI_DIVS: return v / e.a;
+    default: return v;
+  }
+}
+
+__device__ __forceinline__ float in_apply(const ptk_conv_desc &d, long long off_b, long long idx) {
+  float v = d.x[off_b + idx];
+  if (d.in_op == PTK_IN_LEAKY) {
+    v = v >= 0.0f ? v : d.in_a * v;
+  } else if (d.in_op == PTK_IN_AVG3_LEAKY) {
+    v = ((v + d.x1[off_b + idx]) + d.x2[off_b + idx]) / 3.0f;
+    v = v >= 0.0f ? v : d.in_a * v;
+  }
+  return v;
+}
+
+// ------------------------------------------------------------------------------ MFMA conv kernel
+struct ConvGroup {
+  ptk_conv_desc d[PTK_MAX_GROUP];
+  int start[PTK_MAX_GROUP + 1];   // first workgroup of each problem
+  int mt[PTK_MAX_GROUP];          // 32-row blocks per problem
+  int nt[PTK_MAX_GROUP];          // column tiles per problem
+  int ngroup;
+};
+
+// smallest pitch >= w with pitch % 64 == 32: the two 32-lane halves of a wave read rows 2p and
+// 2p+1 of the window at the same column, and this pitch puts them in disjoint LDS bank halves.
+__device__ __host__ __forceinline__ int win_pitch(int w) {
+  return w <= 32 ? 32 : 32 + (w - 32 + 63) / 64 * 64;
+}
+
+template <int KT, int NB>
+__global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
+  extern __shared__ float smem[];
+  int bid = blockIdx.x;
+  int p = 0;
+#pragma unroll
+  for (int i = 1; i < PTK_MAX_GROUP; i++)
+    if (i < g.ngroup && bid >= g.start[i]) p = i;
+  const ptk_conv_desc &d = g.d[p];
+  bid -= g.start[p];
+  const int mt = g.mt[p], nt = g.nt[p];
+  const int b = bid / (mt * nt);
+  bid -= b * mt * nt;
+  const int mb = bid % mt;
+  const int tn = bid / mt;
+
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int half = lane >> 5;     // which of the two reduction rows this lane feeds
+  const int l32 = lane & 31;
+  const int K = KT ? KT : d.K;
+  const int dil = d.dil, st = d.stride;
+  const long long q0 = d.q0 + (long long) tn * (32 * NB);
+  const int kd = (K - 1) * dil;
+  const int dmin = kd < 0 ? kd : 0;
+  const int XW = (32 * NB - 1) * st + (kd < 0 ? -kd : kd) + 1;
+  const int XWP = win_pitch(XW);
+  const long long cmin = q0 * st + dmin - d.shift;
+  const int cw = d.cinp / CONV_WAVES;
+  const int cbeg = w * cw;
+  const long long xoff = (long long) b * d.bsx;
+  float *xs = smem + w * (CONV_CK * XWP);
+
+  // prefetch registers: lane owns columns lane, lane+64, lane+128 of each of the CK rows
+  constexpr int NJ = CONV_XWMAX / 64;
+  float pf[CONV_CK][NJ];
+  auto load_chunk = [&](int c0) {
+#pragma unroll
+    for (int r = 0; r < CONV_CK; r++) {
+      const int ci = c0 + r;
+#pragma unroll
+      for (int jj = 0; jj < NJ; jj++) {
+        const int col = lane + 64 * jj;
+        const long long c = cmin + col;
+        float v = 0.0f;
+        if (col < XW && ci < d.cin && c >= 0 && c < d.lim) {
+          const long long pc = d.reflect_l1 ? (c == 0 ? 1 : c - 1) : c;
+          v = in_apply(d, xoff, (long long) ci * d.ldx + pc);
+        }
+        pf[r][jj] = v;
+      }
+    }
+  };
+
+  f32x16 acc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[nb][v] = 0.0f;
+
+  const float *wrow = d.w + ((long long) mb * K) * d.cinp * 32 + l32;
+  load_chunk(cbeg);
+  for (int c0 = cbeg; c0 < cbeg + cw; c0 += CONV_CK) {
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int r = 0; r < CONV_CK; r++)
+#pragma unroll
+      for (int jj = 0; jj < NJ; jj++) {
+        const int col = lane + 64 * jj;
+        if (col < XW) xs[r * XWP + col] = pf[r][jj];
+      }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (c0 + CONV_CK < cbeg + cw) load_chunk(c0 + CONV_CK);
+    for (int k = 0; k < K; k++) {
+      const float *wk = wrow + ((long long) k * d.cinp + c0 + half) * 32;
+      const int xcol = l32 * st + k * dil - dmin;
+#pragma unroll
+      for (int pp = 0; pp < CONV_CK / 2; pp++) {
+        const float a = wk[pp * 64];
+        const float *xr = xs + (2 * pp + half) * XWP + xcol;
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++)
+          acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, xr[32 * nb * st], acc[nb], 0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  // deterministic cross-wave reduction through LDS: partial sums added in wave order 0..3
+  __syncthreads();
+  float *red = smem;
+#pragma unroll
+  for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) red[((w * NB + nb) * 16 + v) * 64 + lane] = acc[nb][v];
+  __syncthreads();
+  const long long qend = d.q0 + d.nq;
+#pragma unroll
+  for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+    for (int vv = 0; vv < 4; vv++) {
+      const int v = 4 * w + vv;
+      float s = red[((0 * NB + nb) * 16 + v) * 64 + lane];
+      s += red[((1 * NB + nb) * 16 + v) * 64 + lane];
+      s += red[((2 * NB + nb) * 16 + v) * 64 + lane];
+      s += red[((3 * NB + nb) * 16 + v) * 64 + lane];
+      const int m = mb * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+      const long long q = q0 + 32 * nb + l32;
+      if (m >= d.M || q >= qend) continue;
+      const int co = m % d.C4, r = m / d.C4;
+      const long long col = q * d.ys + r - d.ypad;
+      if (col < 0 || col >= d.Lout) continue;
+      float val = s + ((d.bias != nullptr && co < d.nbias) ? d.bias[co] : 0.0f);
+      for (int e = 0; e < d.nepi; e++) val = epi_apply(val, d.epi[e], b, co, col);
+      d.y[(long long) b * d.bsy + (long long) co * d.ldy + col] = val;
+    }
+}
+
+static int conv_window(const ptk_conv_desc *d, int nb) {
+  const int kd = (d->K - 1) * d->dil;
+  return (32 * nb - 1) * d->stride + (kd < 0 ? -kd : kd) + 1;
+}
+
+static int choose_nb(const ptk_conv_desc *d) {
+  static int env_nb = -1;
+  if (env_nb < 0) {
+    const char *e = getenv("PTK_CONV_NB");
+    env_nb = e ? atoi(e) : 0;
+  }
+  if ((env_nb == 1 || env_nb == 2) && conv_window(d, env_nb) <= CONV_XWMAX) return env_nb;
+  // two column blocks per wave halve the weight traffic per flop; use them when the grid still
+  // has about one workgroup per CU
+  const long long mt = (d->M + 31) / 32;
+  const long long t2 = mt * ((d->nq + 63) / 64) * d->batch;
+  if (t2 >= 224 && conv_window(d, 2) <= CONV_XWMAX) return 2;
+  return 1;
+}
+
+extern "C" int ptk_conv_mfma_ok(const ptk_conv_desc *d) {
+  if (d->M < 16 || d->cin < 2 || d->K < 1 || d->stride < 1 || d->dil == 0) return 0;
+  if (conv_window(d, 1) > CONV_XWMAX) return 0;
+  if (d->cinp != ptk_conv_cinp(d->cin)) return 0;
+  return 1;
+}
+
+template <int KT, int NB>
+static void launch_conv(const ConvGroup &g, int nblk, size_t lds, hipStream_t s) {
+  hipLaunchKernelGGL((conv_mfma_kernel<KT, NB>), dim3((unsigned) nblk), dim3(256), lds, s, g);
+}
+
+extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream) {
+  if (ngroup < 1 || ngroup > PTK_MAX_GROUP) {
+    set_err("ptk_conv_launch: ngroup %d out of range", ngroup);
+    return -1;
+  }
+  ConvGroup g;
+  memset(&g, 0, sizeof g);
+  // heaviest problems first, so their long workgroups start before the short ones
+  int order[PTK_MAX_GROUP];
+  for (int i = 0; i < ngroup; i++) order[i] = i;
+  for (int i = 0; i < ngroup; i++)
+    for (int j = i + 1; j < ngroup; j++)
+      if ((long long) dd[order[j]].K * dd[order[j]].cinp > (long long) dd[order[i]].K * dd[order[i]].cinp) {
+        const int t = order[i];
+        order[i] = order[j];
+        order[j] = t;
+      }
+  const int nb = choose_nb(&dd[order[0]]);
+  int kt = dd[order[0]].K;
+  int total = 0, maxw = 0;
+  for (int i = 0; i < ngroup; i++) {
+    const ptk_conv_desc *d = &dd[order[i]];
+    if (!ptk_conv_mfma_ok(d) || conv_window(d, nb) > CONV_XWMAX) {
+      set_err("ptk_conv_launch: shape outside the MFMA kernel (M %d cin %d K %d dil %d stride %d)",
+              d->M, d->cin, d->K, d->dil, d->stride);
+      return -1;
+    }
+    if (d->nq <= 0 || d->batch <= 0) continue;
+    if (d->K != kt) kt = 0;
+    g.d[g.ngroup] = *d;
+    g.mt[g.ngroup] = (d->M + 31) / 32;
+    g.nt[g.ngroup] = (int) ((d->nq + 32 * nb - 1) / (32 * nb));
+    g.start[g.ngroup] = total;
+    total += g.mt[g.ngroup] * g.nt[g.ngroup] * d->batch;
+    const int xw = conv_window(d, nb);
+    if (xw > maxw) maxw = xw;
+    g.ngroup++;
+  }
+  for (int i = g.ngroup; i <= PTK_MAX_GROUP; i++)
+    if (i < PTK_MAX_GROUP + 1) g.start[i] = total;
+  if (total == 0) return 0;
+  const size_t stage = (size_t) CONV_WAVES * CONV_CK * win_pitch(maxw) * sizeof(float);
+  const size_t redb = (size_t) CONV_WAVES * 16 * nb * 64 * sizeof(float);
+  const size_t lds = stage > redb ? stage : redb;
+  hipStream_t s = (hipStream_t) stream;
+  if (nb == 2) {
+    switch (kt) {
+      case 3: launch_conv<3, 2>(g, total, lds, s); break;
+      case 7: launch_conv<7, 2>(g, total, lds, s); break;
+      case 11: launch_conv<11, 2>(g, total, lds, s); break;
+      default: launch_conv<0, 2>(g, total, lds, s); break;
+    }
+  } else {
+    switch (kt) {
+      case 3: launch_conv<3, 1>(g, total, lds, s); break;
+      case 4: launch_conv<4, 1>(g, total, lds, s); break;
+      case 7: launch_conv<7, 1>(g, total, lds, s); break;
+      case 11: launch_conv<11, 1>(g, total, lds, s); break;
+      default: launch_conv<0, 1>(g, total, lds, s); break;
+    }
+  }
+  HCHK(hipGetLastError());
+  return 0;
+}
+
+// ------------------------------------------------------------------------------ SIMT fallbacks
+// Narrow problems (the cout = 1..15 convs of the tail, 1-channel inputs): one thread per output,
+// summing over tap then channel onto the bias in the reference's order.
+__global__ void conv_simt_kernel(const float *__restrict__ x, long long ldx, long long bsx,
+                                 long long lim, int cin, const float *__restrict__ wp,
+                                 const float *__restrict__ bias, int cout, int K, int st, int dil,
+                                 int shift, float *__restrict__ y, long long ldy, long long bsy,
+                                 long long n, int epi0, float a0, int epi1, float a1) {
+  const long long t = (long long) blockIdx.x * blockDim.x + threadIdx.x;
+  const int m = blockIdx.y, b = blockIdx.z;
+  if (t >= n) return;
+  const float *xb = x + (long long) b * bsx;
+  const float *wq = wp + (long long) (m >> 2) * K * cin * 4 + (m & 3);
+  float v = (bias != nullptr && m < cout) ? bias[m] : 0.0f;
+  for (int k = 0; k < K; k++) {
+    const long long c = t * st + (long long) k * dil - shift;
+    if (c < 0 || c >= lim) continue;
+    const float *wk = wq + (long long) k * cin * 4;
+    for (int ci = 0; ci < cin; ci++) v += wk[ci * 4] * xb[(long long) ci * ldx + c];
+  }
+  ptk_epi e0 = {epi0, a0, nullptr, 0, 0}, e1 = {epi1, a1, nullptr, 0, 0};
+  if (epi0) v = epi_apply(v, e0, b, m, t);
+  if (epi1) v = epi_apply(v, e1, b, m, t);
+  y[(long long) b * bsy + (long long) m * ldy + t] = v;
+}
+
+extern "C" int ptk_conv_simt(const float *x, int64_t ldx, int64_t bsx, int64_t lim, int cin,
+                             const float *wp, const float *bias, int cout, int K, int stride,
+                             int dil, int shift, float *y, int64_t ldy, int64_t bsy, int64_t n,
+                             int batch, int epi0, float a0, int epi1, float a1, void *s) {
+  if (n <= 0 || batch <= 0) return 0;
+  const int c4 = (cout + 3) / 4 * 4;
+  dim3 grid((unsigned) ((n + 255) / 256), (unsigned) c4, (unsigned) batch);
+  hipLaunchKernelGGL(conv_simt_kernel, grid, dim3(256), 0, (hipStream_t) s, x, (long long) ldx,
+                     (long long) bsx, (long long) lim, cin, wp, bias, cout, K, stride, dil, shift,
+                     y, (long long) ldy, (long long) bsy, (long long) n, epi0, a0, epi1, a1);
+  HCHK(hipGetLastError());
+  return 0;
+}
+
+__global__ void convT_simt_kernel(const float *__restrict__ x, long long ldx, long long bsx,
+                                  long long tin, int cin, const float *__restrict__ wp,
+                                  const float *__restrict__ bias, int cout, int s, int pad, int ntap,
+                                  float *__restrict__ y, long long ldy, long long bsy, long long Lout) {
+  const long long oi = (long long) blockIdx.x * blockDim.x + threadIdx.x;
+  const int co = blockIdx.y, b = blockIdx.z;
+  if (oi >= Lout) return;
+  const int c4 = (cout + 3) / 4 * 4;
+  const long long u = oi + pad;
+  const long long q = u / s;
+  const int r = (int) (u - q * s);
+  const int row = r * c4 + co;
+  const float *wq = wp + (long long) (row >> 2) * ntap * cin * 4 + (row & 3);
+  const float *xb = x + (long long) b * bsx;
+  float v = (bias != nullptr && co < cout) ? bias[co] : 0.0f;
+  for (int j = 0; j < ntap; j++) {
+    const long long c = q - j;
+    if (c < 0 || c >= tin) continue;
+    const float *wj = wq + (long long) j * cin * 4;
+    for (int ci = 0; ci < cin; ci++) v += wj[ci * 4] * xb[(long long) ci * ldx + c];
+  }
+  y[(long long) b * bsy + (long long) co * ldy + oi] = v;
+}
+
+extern "C" int ptk_convT_simt(const float *x, int64_t ldx, int64_t bsx, int64_t tin, int cin,
+                              const float *wp, const float *bias, int cout, int st, int pad, int K,
+                              float *y, int64_t ldy, int64_t bsy, int64_t Lout, int batch, void *s) {
+  if (Lout <= 0 || batch <= 0) return 0;
+  const int c4 = (cout + 3) / 4 * 4;
+  const int ntap = (K + st - 1) / st;
+  dim3 grid((unsigned) ((Lout + 255) / 256), (unsigned) c4, (unsigned) batch);
+  hipLaunchKernelGGL(convT_simt_kernel, grid, dim3(256), 0, (hipStream_t) s, x, (long long) ldx,
+                     (long long) bsx, (long long) tin, cin, wp, bias, cout, st, pad, ntap, y,
+                     (long long) ldy, (long long) bsy, (long long) Lout);
+  HCHK(hipGetLastError());
+  return 0;
+}
+
+// ------------------------------------------------------------------------------ matmul
+__global__ void matmul_kernel(const float *__restrict__ A, long long m, long long k, long long lda,
+                              const float *__restrict__ B, long long ldb, long long nn,
+                              float *__restrict__ C, long long ldc) {
+  const long long j = (long long) blockIdx.x * blockDim.x + threadIdx.x;
+  const long long i = blockIdx.y;
+  if (j >= nn || i >= m) return;
+  const float *ar = A + i * lda;
+  float v = 0.0f;
+  for (long long p = 0; p < k; p++) v += ar[p] * B[p * ldb + j];
+  C[i * ldc + j] = v;
+}
+extern "C" int ptk_matmul(const float *A, int64_t m, int64_t k, int64_t lda, const float *B,
+                          int64_t ldb, int64_t nn, float *C, int64_t ldc, void *s) {
+  if (m <= 0 || nn <= 0) return 0;
+  if (m > 65535) {
+    set_err("ptk_matmul: m %lld above the grid limit", (long long) m);
+    return -1;
+  }
+  hipLaunchKernelGGL(matmul_kernel, dim3((unsigned) ((nn + 255) / 256), (unsigned) m), dim3(256), 0,
+                     (hipStream_t) s, A, (long long) m, (long long) k, (long long) lda, B,
+                     (long long) ldb, (long long) nn, C, (long long) ldc);
+  HCHK(hipGetLastError());
+  return 0;
+}
+
+// ------------------------------------------------------------------------------ elementwise
+__global__ void add_kernel(const float *__restrict__ a, const float *__restrict__ b,
+                           float *__restrict__ y, long long n, int epi, float alpha) {
+  long long i = (long long) blockIdx.x * blockDim.x + threadIdx.x;
+  const long long st = (long long) gridDim.x * blockDim.x;
+  for (; i < n; i += st) {
+    float v = a[i] + b[i];
+    if (epi == 1) v = v >= 0.0f ? v : alpha * v;
+    y[i] = v;
+  }
+}
+__global__ void leaky_kernel(const float *__restrict__ a, float *__restrict__ y, long long n,
+                             float alpha) {
+  long long i = (long long) blockIdx.x * blockDim.x + threadIdx.x;
+  const long long st = (long long) gridDim.x * blockDim.x;
+  for (; i < n; i += st) {
+    const float v = a[i];
+    y[i] = v >= 0.0f ? v : alpha * v;
+  }
+}
+__global__ void avg3_leaky_kernel(const float *__restrict__ a, const float *__restrict__ b,
+                                  const float *__restrict__ c, float *__restrict__ y, long long n,
+                                  float alpha) {
+  long long i = (long long) blockIdx.x * blockDim.x + threadIdx.x;
+  const long long st = (long long) gridDim.x * blockDim.x;
+  for (; i < n; i += st) {
+    const float v = ((a[i] + b[i]) + c[i]) / 3.0f;
+    y[i] = v >= 0.0f ? v : alpha * v;
+  }
+}
+static unsigned ew_blocks(long long n) {
+  long long b = (n + 255) / 256;
+  if (b > 8192) b = 8192;
+  return (unsigned) (b < 1 ? 1 : b);
+}
+extern "C" int ptk_add(const float *a, const float *b, float *y, int64_t n, int epi, float alpha,
+                       void *s) {
+  if (n <= 0) return 0;
+  hipLaunchKernelGGL(add_kernel, dim3(ew_blocks(n)), dim3(256), 0, (hipStream_t) s, a, b, y,
+                     (long long) n, epi, alpha);
+  HCHK(hipGetLastError());
+  return 0;
+}
+extern "C" int ptk_avg3_leaky(const float *a, const float *b, const float *c, float *y, int64_t n,
+                              float alpha, void *s) {
+  if (n <= 0) return 0;
+  hipLaunchKernelGGL(avg3_leaky_kernel, dim3(ew_blocks(n)), dim3(256), 0, (hipStream_t) s, a, b, c,
+                     y, (long long) n, alpha);
+  HCHK(hipGetLastError());
+  return 0;
+}
+extern "C" int ptk_leaky(const float *a, float *y, int64_t n, float alpha, void *s) {
+  if (n <= 0) return 0;
+  hipLaunchKernelGGL(leaky_kernel, dim3(ew_blocks(n)), dim3(256), 0, (hipStream_t) s, a, y,
+                     (long long) n, alpha);
+  HCHK(hipGetLastError());
+  return 0;
+}
+
+// ------------------------------------------------------------------------------ decoder tail
+// conv_post output p [72][L] (channel c = band*18 + k) -> waveform, fused:
+//   frame[b][n][t] = hann[n] * sum_k (re Bc[k][n] + im Bs[k][n]),  re/im = exp(p_k) cos/sin(pi sin(p_9+k))
+//   ola[b][j] = sum_{j-4t in [0,16)} frame[b][j-4t][t];   y[b][i] = ola[b][i+8] / max(wsum[i+8], 1e-9)
+//   wav[o] = sum_b sum_m h[b][m] * 4 * y[b][(o+m-31)/4]   over (o+m-31) = 0 mod 4 in range.
+// One workgroup produces TAIL_OUT consecutive samples; it recomputes the ~TAIL_OUT/16 + 5 frames
+// per band it needs (in LDS), so the whole tail is a single pass over p with no intermediates.
+#define TAIL_OUT 256
+#define TAIL_NY (TAIL_OUT / 4 + 18)
+#define TAIL_NT (TAIL_NY / 4 + 6)
+
+__global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, long long ldp,
+                                                    long long bsp, long long L,
+                                                    float *__restrict__ wav, long long bsw,
+                                                    const float *__restrict__ cst) {
+  __shared__ float s_c[PTK_TAIL_NCONST];
+  __shared__ float s_re[4][TAIL_NT][9], s_im[4][TAIL_NT][9];
+  __shared__ float s_fr[4][TAIL_NT][16];
+  __shared__ float s_y[4][TAIL_NY];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < PTK_TAIL_NCONST; i += 256) s_c[i] = cst[i];
+  const float *hann = s_c, *bc = s_c + 16, *bs = s_c + 160, *h = s_c + 304;
+  const long long Ly = 4 * (L - 1);
+  const long long nout = 4 * Ly;
+  const long long o0 = (long long) blockIdx.x * TAIL_OUT;
+  p += (long long) blockIdx.y * bsp;
+  wav += (long long) blockIdx.y * bsw;
+  // y indices this block needs: i = (o + m - 31) / 4 for o in [o0, o0+TAIL_OUT), m in [0, 63);
+  // >> 2 on a signed value is floor division by 4, also below zero
+  const long long i_lo = (o0 - 31) >> 2;
+  // frames t needed by ola index j = i + 8 >= i_lo + 8: 4t in [j - 15, j]
+  const long long t_lo = (i_lo - 4) >> 2;
+  __syncthreads();
+  // 1) spectra of the needed frames
+  for (int e = tid; e < 4 * TAIL_NT * 9; e += 256) {
+    const int b = e / (TAIL_NT * 9), rem = e % (TAIL_NT * 9), tt = rem / 9, k = rem % 9;
+    const long long t = t_lo + tt;
+    float re = 0.0f, im = 0.0f;
+    if (t >= 0 && t < L) {
+      const float mag = expf(p[(long long) (b * 18 + k) * ldp + t]);
+      const float ph = sinf(p[(long long) (b * 18 + 9 + k) * ldp + t]) * 3.1415927f;
+      re = mag * cosf(ph);
+      im = mag * sinf(ph);
+    }
+    s_re[b][tt][k] = re;
+    s_im[b][tt][k] = im;
+  }
+  __syncthreads();
+  // 2) windowed frames (irfft through the basis)
+  for (int e = tid; e < 4 * TAIL_NT * 16; e += 256) {
+    const int b = e / (TAIL_NT * 16), rem = e % (TAIL_NT * 16), tt = rem / 16, n = rem % 16;
+    float fr = 0.0f, fi = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 9; k++) {
+      fr += s_re[b][tt][k] * bc[k * 16 + n];
+      fi += s_im[b][tt][k] * bs[k * 16 + n];
+    }
+    s_fr[b][tt][n] = (fr + fi) * hann[n];
+  }
+  __syncthreads();
+  // 3) overlap-add, window-sum normalisation, [8:-8] trim
+  for (int e = tid; e < 4 * TAIL_NY; e += 256) {
+    const int b = e / TAIL_NY, ii = e % TAIL_NY;
+    const long long i = i_lo + ii;
+    float yv = 0.0f;
+    if (i >= 0 && i < Ly) {
+      const long long j = i + 8;
+      const int r = (int) (j & 3);
+      const long long qq = j >> 2;
+      float ola = 0.0f, ws = 0.0f;
+      for (int jt = 0; jt < 4; jt++) {   // tap jt: frame t = qq - jt, sample n = r + 4*jt
+        const long long t = qq - jt;
+        if (t < 0 || t >= L) continue;
+        const int n = r + 4 * jt;
+        ola += s_fr[b][(int) (t - t_lo)][n];
+        ws += hann[n] * hann[n];
+      }
+      const float eps = 1e-9f;
+      yv = ola / (ws > eps ? ws : eps);
+    }
+    s_y[b][ii] = yv;
+  }
+  __syncthreads();
+  // 4) PQMF synthesis: zero-insert x4 (gain 4), 63-tap FIR per band, sum of bands
+  const long long o = o0 + tid;
+  if (o >= nout) return;
+  float acc = 0.0f;
+  const int m0 = (int) ((31 - o) & 3);   // first tap with (o + m - 31) % 4 == 0
+  for (int b = 0; b < 4; b++) {
+    for (int m = m0; m < 63; m += 4) {
+      const long long i = (o + m - 31) >> 2;
+      if (i < 0 || i >= Ly) continue;
+      acc += h[b * 63 + m] * (4.0f * s_y[b][(int) (i - i_lo)]);
+    }
+  }
+  wav[o] = acc;
+}
+
+extern "C" int ptk_tail_batched(const float *p, int64_t ldp, int64_t bsp, int64_t L, float *wav,
+                                int64_t bsw, int batch, const float *consts, void *s) {
+  if (L < 2) {
+    set_err("ptk_tail: need at least 2 frames (got %lld)", (long long) L);
+    return -1;
+  }
+  if (batch <= 0) return 0;
+  const long long nout = 16 * (L - 1);
+  const unsigned blocks = (unsigned) ((nout + TAIL_OUT - 1) / TAIL_OUT);
+  hipLaunchKernelGGL(tail_kernel, dim3(blocks, (unsigned) batch), dim3(256), 0, (hipStream_t) s, p,
+                     (long long) ldp, (long long) bsp, (long long) L, wav, (long long) bsw, consts);
+  HCHK(hipGetLastError());
+  return 0;
+}
+extern "C" int ptk_tail(const float *p, int64_t ldp, int64_t L, float *wav, const float *consts,
+                        void *s) {
+  return ptk_tail_batched(p, ldp, 0, L, wav, 0, 1, consts, s);
+}
+
+// ------------------------------------------------------------------------------ MFMA layout probe
+__global__ void mfma_probe_kernel(const float *a, const float *b, float *d) {
+  const int lane = threadIdx.x;
+  f32x16 acc;
+  for (int v = 0; v < 16; v++) acc[v] = 0.0f;
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[(lane & 31) * 2 + (lane >> 5)],
+                                             b[(lane >> 5) * 32 + (lane & 31)], acc, 0, 0, 0);
+  for (int v = 0; v < 16; v++) {
+    const int i = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3), j = lane & 31;
+    d[i * 32 + j] = acc[v];
+  }
+}
+extern "C" int ptk_mfma_probe(const float *a, const float *b, float *d, void *s) {
+  hipLaunchKernelGGL(mfma_probe_kernel, dim3(1), dim3(64), 0, (hipStream_t) s, a, b, d);
+  HCHK(hipGetLastError());
+  return 0;
+}

@@ -1,0 +1,236 @@
+"""GPU parity of the device-resident decoder path (ptd_*) against the CPU oracle, at the BASELINE
+configs: per layer (configs 1, 2), the MRF stacks (config 3), the full decoder (config 4), and the
+concurrent / long-form serving (config 5).
+
+Bars: per layer max |err| <= 1e-4 x RMS; end-to-end SNDR >= 60 dB.
+Size-independent properties at full size: 8 concurrent streams give bit-identical output to one
+stream (the kernels are deterministic), and the overlap-save windowed decode of T = 1500 stays
+>= 60 dB from the full decode."""
+from __future__ import annotations
+
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+import np_ref
+import oracle_lib as ol
+from conftest import load_package
+
+pkg = load_package()
+synth = pkg.synth
+TOL = 1e-4
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[gpu] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def relerr(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b)) / max(np.sqrt(np.mean(b ** 2)), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def env():
+    ctx = pkg.Ctx(arena_mb=2048)
+    ws, bs = synth.decoder_weights(1234)
+    model = pkg.Model(ctx, ws, bs)
+    yield ctx, model, ws, bs
+    model.close()
+    ctx.close()
+
+
+def dev_of(ctx, a):
+    return pkg.DevBuf.of(ctx, a)
+
+
+def test_config1_conv_pre(env):
+    ctx, model, ws, bs = env
+    say("config 1 conv_pre T=226")
+    z = synth.latent(226, 11)
+    ref = ol.conv(z, ws[0], bs[0], 512, 7, 1, 3, 1, 1, 0, 0.1)[0]
+    dz, dy = dev_of(ctx, z), pkg.DevBuf(512 * 226)
+    assert ctx.lib.ptd_layer(ctx.ptr, model.ptr, 0, dz.ptr, 226, 1, dy.ptr, 0.0, 0.1) == 0
+    y = dy.download(ctx).reshape(512, 226)
+    assert relerr(y, ref) < TOL
+    dz.free(); dy.free()
+
+
+def test_config2_ups0_with_input_leaky(env):
+    ctx, model, ws, bs = env
+    say("config 2 ups.0 T=226")
+    x = np.random.default_rng(12).standard_normal((512, 226)).astype(np.float32)
+    ref = ol.convT(np.where(x >= 0, x, np.float32(0.1) * x), ws[1], bs[1], 256, 16, 4, 6)[0]
+    dx, dy = dev_of(ctx, x), pkg.DevBuf(256 * 904)
+    assert ctx.lib.ptd_layer(ctx.ptr, model.ptr, 1, dx.ptr, 226, 1, dy.ptr, 0.1, 0.0) == 0
+    y = dy.download(ctx).reshape(256, 904)
+    assert relerr(y, ref) < TOL
+    dx.free(); dy.free()
+
+
+@pytest.mark.parametrize("layer", [2, 3, 10, 11, 18, 19, 21, 28, 37, 39])
+def test_decoder_layers(env, layer):
+    """Single decoder layers at their decoder shapes (T = 226 frames)."""
+    ctx, model, ws, bs = env
+    g = synth.dec_layer(layer)
+    T = {True: 904, False: 3616}[layer < 20] if layer not in (0, 39) else 3617
+    say(f"layer {layer} {g} T={T}")
+    x = np.random.default_rng(layer).standard_normal((g["cin"], T)).astype(np.float32)
+    ref = ol.conv(x, ws[layer], bs[layer], g["cout"], g["K"], 1, g["pad"], g["d"])[0]
+    c4 = (g["cout"] + 3) // 4 * 4
+    dx, dy = dev_of(ctx, x), pkg.DevBuf(c4 * T)
+    assert ctx.lib.ptd_layer(ctx.ptr, model.ptr, layer, dx.ptr, T, 1, dy.ptr, 0.0, 0.0) == 0
+    y = dy.download(ctx).reshape(c4, T)
+    assert relerr(y, ref) < TOL
+    dx.free(); dy.free()
+
+
+@pytest.mark.parametrize("stage,C_,T", [(0, 256, 904), (1, 128, 3616)])
+def test_config3_mrf(env, stage, C_, T):
+    ctx, model, ws, bs = env
+    say(f"config 3 MRF stage {stage} C={C_} T={T}")
+    x = np.random.default_rng(30 + stage).standard_normal((C_, T)).astype(np.float32)
+    base = 2 if stage == 0 else 21
+    ref = ol.mrf(ws[base:base + 18], bs[base:base + 18], x, 0.1)
+    dx, dy = dev_of(ctx, x), pkg.DevBuf(C_ * T)
+    assert ctx.lib.ptd_mrf(ctx.ptr, model.ptr, stage, dx.ptr, T, 0.1, dy.ptr) == 0
+    y = dy.download(ctx).reshape(C_, T)
+    assert relerr(y, ref) < TOL
+    dx.free(); dy.free()
+
+
+def _decode(ctx, model, z, stages=False):
+    T = z.shape[-1]
+    dz = dev_of(ctx, z)
+    dw = pkg.DevBuf(256 * T)
+    if stages:
+        lens = [ol.oracle().orc_dec_stage_len(i, T) for i in range(6)]
+        sb = [pkg.DevBuf(n) for n in lens]
+        arr = (C.c_void_p * 6)(*[b.ptr for b in sb])
+        assert ctx.lib.ptd_decode_stages(ctx.ptr, model.ptr, dz.ptr, T, dw.ptr, arr) == 0
+    else:
+        assert ctx.lib.ptd_decode(ctx.ptr, model.ptr, dz.ptr, T, 1, dw.ptr) == 0
+    wav = dw.download(ctx)
+    out = (wav, [b.download(ctx) for b in sb]) if stages else wav
+    dz.free(); dw.free()
+    if stages:
+        for b in sb:
+            b.free()
+    return out
+
+
+@pytest.mark.parametrize("T", [5, 37])
+def test_decoder_small_vs_oracle(env, T):
+    ctx, model, ws, bs = env
+    say(f"decoder T={T}")
+    z = synth.latent(T, 100 + T)
+    ref, rst = ol.decoder(ws, bs, z, stages=True)
+    wav, st = _decode(ctx, model, z, stages=True)
+    for i in range(6):
+        assert relerr(st[i], rst[i]) < TOL, f"stage {i}"
+    assert np_ref.sndr(wav, ref) >= 60.0
+
+
+def test_config4_decoder_T226_vs_oracle(env):
+    ctx, model, ws, bs = env
+    say("config 4 decoder T=226")
+    z = synth.latent(226, 226)
+    ref = ol.decoder(ws, bs, z)
+    wav = _decode(ctx, model, z)
+    assert wav.shape == (57856,)
+    assert np_ref.sndr(wav, ref) >= 60.0
+
+
+def test_batched_decode_matches_single(env):
+    """batch > 1 (used by the windowed path) equals per-item decodes bit for bit."""
+    ctx, model, ws, bs = env
+    say("batched decode")
+    T = 24
+    zs = [synth.latent(T, 500 + i) for i in range(3)]
+    singles = [_decode(ctx, model, z) for z in zs]
+    dz = dev_of(ctx, np.stack(zs))
+    dw = pkg.DevBuf(3 * 256 * T)
+    assert ctx.lib.ptd_decode(ctx.ptr, model.ptr, dz.ptr, T, 3, dw.ptr) == 0
+    wb = dw.download(ctx).reshape(3, 256 * T)
+    for i in range(3):
+        assert np.array_equal(wb[i], singles[i])
+    dz.free(); dw.free()
+
+
+def _oracle_windows(ws, bs, z, win, ctx_):
+    """The reference's overlap-save schedule (main_v21_serve.c:229-257) composed on the oracle."""
+    T = z.shape[-1]
+    out = np.zeros(256 * T, np.float32)
+    a = emitted = 0
+    while emitted < T:
+        w = min(win, T - a)
+        last = a + w >= T
+        lo = 0 if a == 0 else ctx_
+        hi = w if last else w - ctx_
+        e0, e1 = max(a + lo, emitted), min(a + hi, T)
+        pcm = ol.decoder(ws, bs, np.ascontiguousarray(z[:, a:a + w]))
+        if e1 > e0:
+            out[e0 * 256:e1 * 256] = pcm[(e0 - a) * 256:(e1 - a) * 256]
+            emitted = e1
+        if last:
+            break
+        a = max(e1 - ctx_, 1)
+    return out
+
+
+def test_windows_small_vs_oracle(env):
+    ctx, model, ws, bs = env
+    say("windows T=70 win=32 ctx=8")
+    T, win, cx = 70, 32, 8
+    z = synth.latent(T, 70)
+    ref = _oracle_windows(ws, bs, z, win, cx)
+    dz, dw = dev_of(ctx, z), pkg.DevBuf(256 * T)
+    assert ctx.lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, win, cx, dw.ptr) == 0
+    wav = dw.download(ctx)
+    assert np_ref.sndr(wav, ref) >= 60.0
+    dz.free(); dw.free()
+
+
+def test_config5_longform_windows_vs_full(env):
+    """T = 1500 through 96-frame windows with 16-frame context >= 60 dB from one full decode."""
+    ctx, model, ws, bs = env
+    say("config 5 long-form T=1500")
+    T = 1500
+    z = synth.latent(T, 1500)
+    full = _decode(ctx, model, z)
+    dz, dw = dev_of(ctx, z), pkg.DevBuf(256 * T)
+    assert ctx.lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, 96, 16, dw.ptr) == 0
+    wav = dw.download(ctx)
+    assert np_ref.sndr(wav, full) >= 60.0
+    dz.free(); dw.free()
+
+
+def test_config5_concurrent_streams_bitexact(env):
+    """8 requests, T ~ U[56, 400], on 8 contexts/streams sharing one weight set: every stream's
+    output equals the single-stream decode bit for bit, and one of them matches the oracle."""
+    ctx, model, ws, bs = env
+    Ts = synth.request_lengths(5, 8)
+    say(f"config 5 streams T={Ts}")
+    zs = [synth.latent(T, 900 + i) for i, T in enumerate(Ts)]
+    singles = [_decode(ctx, model, z) for z in zs]
+    lib = ctx.lib
+    srv = lib.ptd_server_create(8, 256 << 20)
+    assert srv
+    dz = [dev_of(ctx, z) for z in zs]
+    dw = [pkg.DevBuf(256 * T) for T in Ts]
+    reqs = (pkg.Request * 8)(*[pkg.Request(dz[i].ptr, dw[i].ptr, Ts[i], 0, 0) for i in range(8)])
+    wall = C.c_double()
+    for _ in range(2):
+        assert lib.ptd_serve_run(srv, model.ptr, reqs, 8, C.byref(wall)) == 0
+        for i in range(8):
+            assert np.array_equal(dw[i].download(ctx), singles[i]), f"stream {i}"
+    lib.ptd_server_destroy(srv)
+    i0 = int(np.argmin(Ts))
+    assert np_ref.sndr(singles[i0], ol.decoder(ws, bs, zs[i0])) >= 60.0
+    for b in dz + dw:
+        b.free()
