@@ -138,6 +138,15 @@ def main():
                 raise RuntimeError("mrf depth failed")
         ctx.sync()
         log(f"kernel loop: {2 * args.kernel_loop} launches done")
+        # calibration for the HBM byte counters: add_kernel over 64 Mi floats reads exactly
+        # 512 MiB and writes 256 MiB per launch
+        n = 64 << 20
+        a, b2, y = pkg.DevBuf(n), pkg.DevBuf(n), pkg.DevBuf(n)
+        for _ in range(5):
+            if lib.pt_v21_devadd_run(ctx.ptr, a.ptr, b2.ptr, y.ptr, n, 0, 0.0) != 0:
+                raise RuntimeError("calibration add failed")
+        ctx.sync()
+        log("calibration: 5 add_kernel launches of 64 Mi floats (read 524288 KiB, write 262144 KiB)")
         return
     for _ in range(5):
         run_depth()
