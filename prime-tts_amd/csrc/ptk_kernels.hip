@@ -147,12 +147,15 @@ extern "C" int ptk_device_sync(void) {
 
 // ------------------------------------------------------------------------------ weight relayout
 // Packed [M/4][K][cin][4] (the reference's conv layout; a convT's phase rows are just more rows)
-// -> MFMA operand layout [Mp/32][K][cinp][32]: for a fixed (row block, tap, channel) the 32 rows
-// are contiguous, so the A operand of a 32x32x2 MFMA (32 rows x 2 channels) is two 128-byte
-// segments.  cinp rounds cin up so every wave of the 4-way channel split owns whole chunks.
+// -> MFMA operand layout [Mp/32][K][cinp/8][64][4].  For a row block mb, tap k and a chunk of 8
+// input channels, lane l = 32*h + r of a wave holds the four floats
+//     W[mb*32 + r][k][chunk*8 + 2*p + h],   p = 0..3,
+// which are exactly its A operands (row r, reduction index h) of the four v_mfma_f32_32x32x2_f32
+// that consume channel pairs (2p, 2p+1) of the chunk.  One 16-byte load per lane therefore feeds
+// four MFMAs, and the 1 KiB a wave loads for one (tap, chunk) is contiguous.  cinp rounds cin up
+// so every wave of the 4-way channel split owns whole chunks; padding rows/channels are zero.
 #define CONV_CK 8          // input channels per staged chunk (per wave)
 #define CONV_WAVES 4       // waves per workgroup, each owning a quarter of the channels
-#define CONV_XWMAX 192     // widest input window (columns) a wave stages per channel
 
 extern "C" int ptk_conv_cinp(int cin) {
   const int q = CONV_WAVES * CONV_CK;
@@ -167,14 +170,17 @@ __global__ void relayout_kernel(float *__restrict__ dst, const float *__restrict
                                 int K, int cin, int cinp, long long total) {
   long long i = (long long) blockIdx.x * blockDim.x + threadIdx.x;
   const long long st = (long long) gridDim.x * blockDim.x;
+  const int nchunk = cinp / CONV_CK;
   for (; i < total; i += st) {
-    const int mm = (int) (i & 31);
-    long long r = i >> 5;
-    const int ci = (int) (r % cinp);
-    r /= cinp;
+    const int p = (int) (i & 3);
+    const int lane = (int) ((i >> 2) & 63);
+    long long r = i >> 8;
+    const int chunk = (int) (r % nchunk);
+    r /= nchunk;
     const int k = (int) (r % K);
     const int mb = (int) (r / K);
-    const int m = mb * 32 + mm;
+    const int m = mb * 32 + (lane & 31);
+    const int ci = chunk * CONV_CK + 2 * p + (lane >> 5);
     float v = 0.0f;
     if (m < M && ci < cin) v = wp[(((long long) (m >> 2) * K + k) * cin + ci) * 4 + (m & 3)];
     dst[i] = v;
@@ -204,14 +210,12 @@ __device__ __forceinline__ float epi_apply(float v, const ptk_epi &e, int b, int
   }
 }
 
-__device__ __forceinline__ float in_apply(const ptk_conv_desc &d, long long off_b, long long idx) {
-  float v = d.x[off_b + idx];
-  if (d.in_op == PTK_IN_LEAKY) {
-    v = v >= 0.0f ? v : d.in_a * v;
-  } else if (d.in_op == PTK_IN_AVG3_LEAKY) {
-    v = ((v + d.x1[off_b + idx]) + d.x2[off_b + idx]) / 3.0f;
-    v = v >= 0.0f ? v : d.in_a * v;
-  }
+// input transform applied as a window element is staged (the reference's separate LeakyReLU /
+// Add / Div nodes in front of a conv, fused): IN is a PTK_IN_* code
+template <int IN>
+__device__ __forceinline__ float in_xform(float v, float v1, float v2, float a) {
+  if constexpr (IN == PTK_IN_AVG3_LEAKY) v = ((v + v1) + v2) / 3.0f;
+  if constexpr (IN != PTK_IN_PLAIN) v = v >= 0.0f ? v : a * v;
   return v;
 }
 
@@ -224,15 +228,25 @@ struct ConvGroup {
   int ngroup;
 };
 
-// smallest pitch >= w with pitch % 64 == 32: the two 32-lane halves of a wave read rows 2p and
-// 2p+1 of the window at the same column, and this pitch puts them in disjoint LDS bank halves.
-__device__ __host__ __forceinline__ int win_pitch(int w) {
-  return w <= 32 ? 32 : 32 + (w - 32 + 63) / 64 * 64;
-}
+// Staged input window of one channel row: NB column blocks of 32 outputs need
+// (32*NB - 1)*stride + |K-1|*|dil| + 1 columns.  The kernel supports up to 64*(NB+1) columns and
+// lays rows out with pitch 64*(NB+1) + 32: the two 32-lane halves of a wave read rows 2p and 2p+1
+// at the same column, and a pitch = 32 (mod 64) puts them in disjoint bank halves.  The pitch is a
+// compile-time constant so every LDS read of the inner loop is one instruction with an immediate
+// offset.
+template <int NB> struct WinGeo {
+  static constexpr int NJ = NB + 1;          // 64-column slices a lane loads per row
+  static constexpr int XWMAX = 64 * NJ;
+  static constexpr int XWP = XWMAX + 32;
+};
 
-template <int KT, int NB>
+// KT > 0: the group's taps are all <= KT and the whole chunk's A operands (KT float4 per lane) are
+// prefetched one chunk ahead; KT == 0: any K, A loaded per tap.  IN: input transform (PTK_IN_*).
+template <int KT, int NB, int IN>
 __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   extern __shared__ float smem[];
+  constexpr int NJ = WinGeo<NB>::NJ, XWP = WinGeo<NB>::XWP;
+  constexpr int NX = IN == PTK_IN_AVG3_LEAKY ? 3 : 1;
   int bid = blockIdx.x;
   int p = 0;
 #pragma unroll
@@ -246,40 +260,72 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   const int mb = bid % mt;
   const int tn = bid / mt;
 
+  // descriptor fields used in loops, read once (the problem index is dynamic, so the compiler
+  // would otherwise re-read them from the kernel arguments)
+  const int K = d.K, dil = d.dil, st = d.stride, cin = d.cin;
+  const unsigned ldx = (unsigned) d.ldx;
+  const long long lim = d.lim;
+  const float in_a = d.in_a;
+  const int nchunk = d.cinp / CONV_CK;          // chunks over all channels
+  const int nch = nchunk / CONV_WAVES;          // chunks of this wave
+
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int half = lane >> 5;     // which of the two reduction rows this lane feeds
   const int l32 = lane & 31;
-  const int K = KT ? KT : d.K;
-  const int dil = d.dil, st = d.stride;
   const long long q0 = d.q0 + (long long) tn * (32 * NB);
   const int kd = (K - 1) * dil;
   const int dmin = kd < 0 ? kd : 0;
   const int XW = (32 * NB - 1) * st + (kd < 0 ? -kd : kd) + 1;
-  const int XWP = win_pitch(XW);
   const long long cmin = q0 * st + dmin - d.shift;
-  const int cw = d.cinp / CONV_WAVES;
-  const int cbeg = w * cw;
-  const long long xoff = (long long) b * d.bsx;
+  const int chunk0 = w * nch;
   float *xs = smem + w * (CONV_CK * XWP);
 
-  // prefetch registers: lane owns columns lane, lane+64, lane+128 of each of the CK rows
-  constexpr int NJ = CONV_XWMAX / 64;
-  float pf[CONV_CK][NJ];
+  // Window columns this lane stages (fixed for the workgroup): validity and physical column.
+  // An out-of-range element reads offset 0 of its batch item (always valid) and is zeroed.
+  const long long xoff = (long long) b * d.bsx;
+  const float *xb = d.x + xoff;
+  const float *xb1 = NX == 3 ? d.x1 + xoff : xb;
+  const float *xb2 = NX == 3 ? d.x2 + xoff : xb;
+  unsigned pcol[NJ];
+  bool cok[NJ];
+#pragma unroll
+  for (int jj = 0; jj < NJ; jj++) {
+    const int col = lane + 64 * jj;
+    const long long c = cmin + col;
+    cok[jj] = (col < XW) & (c >= 0) & (c < lim);
+    const long long pc = d.reflect_l1 ? (c == 0 ? 1 : c - 1) : c;
+    pcol[jj] = cok[jj] ? (unsigned) pc : 0u;
+  }
+
+  // Staging is split so that all global loads of a chunk are in flight together: the load phase
+  // only issues loads, the store phase (one chunk later) masks, transforms and writes LDS.
+  float pf[NX][CONV_CK][NJ];
   auto load_chunk = [&](int c0) {
 #pragma unroll
     for (int r = 0; r < CONV_CK; r++) {
-      const int ci = c0 + r;
+      const unsigned rowo = c0 + r < cin ? (unsigned) (c0 + r) * ldx : 0u;
 #pragma unroll
       for (int jj = 0; jj < NJ; jj++) {
-        const int col = lane + 64 * jj;
-        const long long c = cmin + col;
-        float v = 0.0f;
-        if (col < XW && ci < d.cin && c >= 0 && c < d.lim) {
-          const long long pc = d.reflect_l1 ? (c == 0 ? 1 : c - 1) : c;
-          v = in_apply(d, xoff, (long long) ci * d.ldx + pc);
+        const unsigned o = rowo + pcol[jj];
+        pf[0][r][jj] = xb[o];
+        if constexpr (NX == 3) {
+          pf[1][r][jj] = xb1[o];
+          pf[2][r][jj] = xb2[o];
         }
-        pf[r][jj] = v;
+      }
+    }
+  };
+  auto store_chunk = [&](int c0) {
+#pragma unroll
+    for (int r = 0; r < CONV_CK; r++) {
+      const bool rok = c0 + r < cin;
+#pragma unroll
+      for (int jj = 0; jj < NJ; jj++) {
+        float v;
+        if constexpr (NX == 3) v = in_xform<IN>(pf[0][r][jj], pf[1][r][jj], pf[2][r][jj], in_a);
+        else v = in_xform<IN>(pf[0][r][jj], 0.0f, 0.0f, in_a);
+        xs[r * XWP + lane + 64 * jj] = (rok & cok[jj]) ? v : 0.0f;
       }
     }
   };
@@ -290,31 +336,56 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[nb][v] = 0.0f;
 
-  const float *wrow = d.w + ((long long) mb * K) * d.cinp * 32 + l32;
-  load_chunk(cbeg);
-  for (int c0 = cbeg; c0 < cbeg + cw; c0 += CONV_CK) {
+  // A operands: float4 index ((mb*K + k)*nchunk + chunk)*64 + lane
+  const float4 *wa = reinterpret_cast<const float4 *>(d.w) +
+                     ((long long) mb * K * nchunk + chunk0) * 64 + lane;
+  const int wtap = nchunk * 64;   // float4 stride between taps
+  constexpr int KA = KT > 0 ? KT : 1;
+  float4 acur[KA];
+  if constexpr (KT > 0) {
+#pragma unroll
+    for (int k = 0; k < KT; k++)
+      if (k < K) acur[k] = wa[k * wtap];
+  }
+  load_chunk(chunk0 * CONV_CK);
+  const int lbase = half * XWP + l32 * st - dmin;
+  for (int j = 0; j < nch; j++) {
     __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int r = 0; r < CONV_CK; r++)
-#pragma unroll
-      for (int jj = 0; jj < NJ; jj++) {
-        const int col = lane + 64 * jj;
-        if (col < XW) xs[r * XWP + col] = pf[r][jj];
-      }
+    store_chunk((chunk0 + j) * CONV_CK);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (c0 + CONV_CK < cbeg + cw) load_chunk(c0 + CONV_CK);
-    for (int k = 0; k < K; k++) {
-      const float *wk = wrow + ((long long) k * d.cinp + c0 + half) * 32;
-      const int xcol = l32 * st + k * dil - dmin;
+    const bool more = j + 1 < nch;
+    if (more) load_chunk((chunk0 + j + 1) * CONV_CK);
+    if constexpr (KT > 0) {
 #pragma unroll
-      for (int pp = 0; pp < CONV_CK / 2; pp++) {
-        const float a = wk[pp * 64];
-        const float *xr = xs + (2 * pp + half) * XWP + xcol;
+      for (int k = 0; k < KT; k++) {
+        if (k < K) {   // predicated, not break: the loop must unroll so acur stays in registers
+          const float4 a = acur[k];
+          if (more) acur[k] = wa[k * wtap + (j + 1) * 64];
+          const float *xr = xs + lbase + k * dil;
 #pragma unroll
-        for (int nb = 0; nb < NB; nb++)
-          acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, xr[32 * nb * st], acc[nb], 0, 0, 0);
+          for (int nb = 0; nb < NB; nb++) {
+            const float *xq = xr + 32 * nb * st;
+            acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, xq[0], acc[nb], 0, 0, 0);
+            acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, xq[2 * XWP], acc[nb], 0, 0, 0);
+            acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, xq[4 * XWP], acc[nb], 0, 0, 0);
+            acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, xq[6 * XWP], acc[nb], 0, 0, 0);
+          }
+        }
+      }
+    } else {
+      for (int k = 0; k < K; k++) {
+        const float4 a = wa[k * wtap + j * 64];
+        const float *xr = xs + lbase + k * dil;
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) {
+          const float *xq = xr + 32 * nb * st;
+          acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, xq[0], acc[nb], 0, 0, 0);
+          acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, xq[2 * XWP], acc[nb], 0, 0, 0);
+          acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, xq[4 * XWP], acc[nb], 0, 0, 0);
+          acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, xq[6 * XWP], acc[nb], 0, 0, 0);
+        }
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -354,6 +425,8 @@ static int conv_window(const ptk_conv_desc *d, int nb) {
   const int kd = (d->K - 1) * d->dil;
   return (32 * nb - 1) * d->stride + (kd < 0 ? -kd : kd) + 1;
 }
+static int win_max(int nb) { return nb == 2 ? WinGeo<2>::XWMAX : WinGeo<1>::XWMAX; }
+static int win_pitch(int nb) { return nb == 2 ? WinGeo<2>::XWP : WinGeo<1>::XWP; }
 
 static int choose_nb(const ptk_conv_desc *d) {
   static int env_nb = -1;
@@ -361,25 +434,42 @@ static int choose_nb(const ptk_conv_desc *d) {
     const char *e = getenv("PTK_CONV_NB");
     env_nb = e ? atoi(e) : 0;
   }
-  if ((env_nb == 1 || env_nb == 2) && conv_window(d, env_nb) <= CONV_XWMAX) return env_nb;
+  if ((env_nb == 1 || env_nb == 2) && conv_window(d, env_nb) <= win_max(env_nb)) return env_nb;
   // two column blocks per wave halve the weight traffic per flop; use them when the grid still
   // has about one workgroup per CU
   const long long mt = (d->M + 31) / 32;
   const long long t2 = mt * ((d->nq + 63) / 64) * d->batch;
-  if (t2 >= 224 && conv_window(d, 2) <= CONV_XWMAX) return 2;
+  if (t2 >= 224 && conv_window(d, 2) <= win_max(2)) return 2;
   return 1;
 }
 
 extern "C" int ptk_conv_mfma_ok(const ptk_conv_desc *d) {
   if (d->M < 16 || d->cin < 2 || d->K < 1 || d->stride < 1 || d->dil == 0) return 0;
-  if (conv_window(d, 1) > CONV_XWMAX) return 0;
+  if (conv_window(d, 1) > win_max(1)) return 0;
   if (d->cinp != ptk_conv_cinp(d->cin)) return 0;
   return 1;
 }
 
-template <int KT, int NB>
+template <int KT, int NB, int IN>
 static void launch_conv(const ConvGroup &g, int nblk, size_t lds, hipStream_t s) {
-  hipLaunchKernelGGL((conv_mfma_kernel<KT, NB>), dim3((unsigned) nblk), dim3(256), lds, s, g);
+  hipLaunchKernelGGL((conv_mfma_kernel<KT, NB, IN>), dim3((unsigned) nblk), dim3(256), lds, s, g);
+}
+
+template <int NB, int IN>
+static void launch_conv_k(int kmax, const ConvGroup &g, int nblk, size_t lds, hipStream_t s) {
+  if (kmax <= 3) launch_conv<3, NB, IN>(g, nblk, lds, s);
+  else if (kmax == 4) launch_conv<4, NB, IN>(g, nblk, lds, s);
+  else if (kmax <= 7) launch_conv<7, NB, IN>(g, nblk, lds, s);
+  else if (kmax <= 11) launch_conv<11, NB, IN>(g, nblk, lds, s);
+  else launch_conv<0, NB, IN>(g, nblk, lds, s);
+}
+
+template <int NB>
+static void launch_conv_in(int in_op, int kmax, const ConvGroup &g, int nblk, size_t lds,
+                           hipStream_t s) {
+  if (in_op == PTK_IN_LEAKY) launch_conv_k<NB, PTK_IN_LEAKY>(kmax, g, nblk, lds, s);
+  else if (in_op == PTK_IN_AVG3_LEAKY) launch_conv_k<NB, PTK_IN_AVG3_LEAKY>(kmax, g, nblk, lds, s);
+  else launch_conv_k<NB, PTK_IN_PLAIN>(kmax, g, nblk, lds, s);
 }
 
 extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream) {
@@ -400,49 +490,38 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
         order[j] = t;
       }
   const int nb = choose_nb(&dd[order[0]]);
-  int kt = dd[order[0]].K;
-  int total = 0, maxw = 0;
+  int kmax = 0, in_op = -1;
+  int total = 0;
   for (int i = 0; i < ngroup; i++) {
     const ptk_conv_desc *d = &dd[order[i]];
-    if (!ptk_conv_mfma_ok(d) || conv_window(d, nb) > CONV_XWMAX) {
+    if (!ptk_conv_mfma_ok(d) || conv_window(d, nb) > win_max(nb)) {
       set_err("ptk_conv_launch: shape outside the MFMA kernel (M %d cin %d K %d dil %d stride %d)",
               d->M, d->cin, d->K, d->dil, d->stride);
       return -1;
     }
     if (d->nq <= 0 || d->batch <= 0) continue;
-    if (d->K != kt) kt = 0;
+    if (in_op < 0) in_op = d->in_op;
+    if (d->in_op != in_op || d->in_op < PTK_IN_PLAIN || d->in_op > PTK_IN_AVG3_LEAKY ||
+        (d->in_op == PTK_IN_AVG3_LEAKY && (!d->x1 || !d->x2))) {
+      set_err("ptk_conv_launch: grouped problems need one valid input transform");
+      return -1;
+    }
+    if (d->K > kmax) kmax = d->K;
     g.d[g.ngroup] = *d;
     g.mt[g.ngroup] = (d->M + 31) / 32;
     g.nt[g.ngroup] = (int) ((d->nq + 32 * nb - 1) / (32 * nb));
     g.start[g.ngroup] = total;
     total += g.mt[g.ngroup] * g.nt[g.ngroup] * d->batch;
-    const int xw = conv_window(d, nb);
-    if (xw > maxw) maxw = xw;
     g.ngroup++;
   }
-  for (int i = g.ngroup; i <= PTK_MAX_GROUP; i++)
-    if (i < PTK_MAX_GROUP + 1) g.start[i] = total;
+  for (int i = g.ngroup; i <= PTK_MAX_GROUP; i++) g.start[i] = total;
   if (total == 0) return 0;
-  const size_t stage = (size_t) CONV_WAVES * CONV_CK * win_pitch(maxw) * sizeof(float);
+  const size_t stage = (size_t) CONV_WAVES * CONV_CK * win_pitch(nb) * sizeof(float);
   const size_t redb = (size_t) CONV_WAVES * 16 * nb * 64 * sizeof(float);
   const size_t lds = stage > redb ? stage : redb;
   hipStream_t s = (hipStream_t) stream;
-  if (nb == 2) {
-    switch (kt) {
-      case 3: launch_conv<3, 2>(g, total, lds, s); break;
-      case 7: launch_conv<7, 2>(g, total, lds, s); break;
-      case 11: launch_conv<11, 2>(g, total, lds, s); break;
-      default: launch_conv<0, 2>(g, total, lds, s); break;
-    }
-  } else {
-    switch (kt) {
-      case 3: launch_conv<3, 1>(g, total, lds, s); break;
-      case 4: launch_conv<4, 1>(g, total, lds, s); break;
-      case 7: launch_conv<7, 1>(g, total, lds, s); break;
-      case 11: launch_conv<11, 1>(g, total, lds, s); break;
-      default: launch_conv<0, 1>(g, total, lds, s); break;
-    }
-  }
+  if (nb == 2) launch_conv_in<2>(in_op, kmax, g, total, lds, s);
+  else launch_conv_in<1>(in_op, kmax, g, total, lds, s);
   HCHK(hipGetLastError());
   return 0;
 }
