@@ -212,10 +212,12 @@ __device__ __forceinline__ float epi_apply(float v, const ptk_epi &e, int b, int
 
 // input transform applied as a window element is staged (the reference's separate LeakyReLU /
 // Add / Div nodes in front of a conv, fused): IN is a PTK_IN_* code
+// LeakyReLU as max(v, a*v): identical to (v >= 0 ? v : a*v) for 0 <= a <= 1 (signed zeros
+// included), which the launcher enforces, in two instructions instead of three.
 template <int IN>
 __device__ __forceinline__ float in_xform(float v, float v1, float v2, float a) {
   if constexpr (IN == PTK_IN_AVG3_LEAKY) v = ((v + v1) + v2) / 3.0f;
-  if constexpr (IN != PTK_IN_PLAIN) v = v >= 0.0f ? v : a * v;
+  if constexpr (IN != PTK_IN_PLAIN) v = fmaxf(v, a * v);
   return v;
 }
 
@@ -226,6 +228,7 @@ struct ConvGroup {
   int mt[PTK_MAX_GROUP];          // 32-row blocks per problem
   int nt[PTK_MAX_GROUP];          // column tiles per problem
   int ngroup;
+  int split;                      // waves of a workgroup sharing one output block: 1, 2 or 4
 };
 
 // Staged input window of one channel row: NB column blocks of 32 outputs need
@@ -240,8 +243,21 @@ template <int NB> struct WinGeo {
   static constexpr int XWP = XWMAX + 32;
 };
 
-// KT > 0: the group's taps are all <= KT and the whole chunk's A operands (KT float4 per lane) are
-// prefetched one chunk ahead; KT == 0: any K, A loaded per tap.  IN: input transform (PTK_IN_*).
+// word 3 of a raw buffer resource on gfx9-family parts (gfx950): 32-bit data, range checked
+#define PTK_BUF_WORD3 0x00020000
+// an offset past every buffer: the load returns 0 (buffer range checking)
+#define PTK_OOB 0x80000000u
+
+__device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+// One workgroup = 4 waves.  The waves form 4/S column groups of S waves; the S waves of a group
+// compute the same 32-row x 32*NB-column output block over disjoint quarters/halves of the input
+// channels (S = 1: each wave its own block over all channels) and are reduced through LDS in wave
+// order (deterministic).  KT > 0: every problem of the group has K <= KT and the whole next chunk's
+// A operands (KT float4 per lane) are prefetched while the current chunk runs; KT == 0: any K, A
+// loaded per tap.  IN: input transform (PTK_IN_*).
 template <int KT, int NB, int IN>
 __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   extern __shared__ float smem[];
@@ -259,75 +275,82 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   bid -= b * mt * nt;
   const int mb = bid % mt;
   const int tn = bid / mt;
+  const int S = g.split, G = 4 / S;
 
   // descriptor fields used in loops, read once (the problem index is dynamic, so the compiler
   // would otherwise re-read them from the kernel arguments)
   const int K = d.K, dil = d.dil, st = d.stride, cin = d.cin;
-  const unsigned ldx = (unsigned) d.ldx;
+  const unsigned ldx4 = (unsigned) d.ldx * 4u;
   const long long lim = d.lim;
   const float in_a = d.in_a;
   const int nchunk = d.cinp / CONV_CK;          // chunks over all channels
-  const int nch = nchunk / CONV_WAVES;          // chunks of this wave
+  const int nch = nchunk / S;                   // chunks of this wave
 
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  // wave index: uniform across the wave, which the compiler cannot see on its own (without this
+  // the wave-based buffer resources would be treated as divergent)
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ks = w % S, cg = w / S;             // channel split index, column group
   const int half = lane >> 5;     // which of the two reduction rows this lane feeds
   const int l32 = lane & 31;
-  const long long q0 = d.q0 + (long long) tn * (32 * NB);
+  const long long q0 = d.q0 + ((long long) tn * G + cg) * (32 * NB);
   const int kd = (K - 1) * dil;
   const int dmin = kd < 0 ? kd : 0;
   const int XW = (32 * NB - 1) * st + (kd < 0 ? -kd : kd) + 1;
   const long long cmin = q0 * st + dmin - d.shift;
-  const int chunk0 = w * nch;
+  const int chunk0 = ks * nch;
   float *xs = smem + w * (CONV_CK * XWP);
 
-  // Window columns this lane stages (fixed for the workgroup): validity and physical column.
-  // An out-of-range element reads offset 0 of its batch item (always valid) and is zeroed.
+  // Window columns this lane stages, fixed for the wave: byte offset in the row, or an offset the
+  // buffer range check turns into 0 (columns outside [0, lim), past the window).  Channels past
+  // cin fall outside the buffer (num_records = cin rows) and read 0 as well.
   const long long xoff = (long long) b * d.bsx;
-  const float *xb = d.x + xoff;
-  const float *xb1 = NX == 3 ? d.x1 + xoff : xb;
-  const float *xb2 = NX == 3 ? d.x2 + xoff : xb;
-  unsigned pcol[NJ];
-  bool cok[NJ];
+  const unsigned nrec = (unsigned) cin * ldx4;
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      (void *) (d.x + xoff), (short) 0, (int) nrec, PTK_BUF_WORD3);
+  __amdgpu_buffer_rsrc_t rx1 = rx, rx2 = rx;
+  if constexpr (NX == 3) {
+    rx1 = __builtin_amdgcn_make_buffer_rsrc((void *) (d.x1 + xoff), (short) 0, (int) nrec, PTK_BUF_WORD3);
+    rx2 = __builtin_amdgcn_make_buffer_rsrc((void *) (d.x2 + xoff), (short) 0, (int) nrec, PTK_BUF_WORD3);
+  }
+  unsigned voff[NJ];
 #pragma unroll
   for (int jj = 0; jj < NJ; jj++) {
     const int col = lane + 64 * jj;
     const long long c = cmin + col;
-    cok[jj] = (col < XW) & (c >= 0) & (c < lim);
+    const bool ok = (col < XW) & (c >= 0) & (c < lim);
     const long long pc = d.reflect_l1 ? (c == 0 ? 1 : c - 1) : c;
-    pcol[jj] = cok[jj] ? (unsigned) pc : 0u;
+    voff[jj] = ok ? (unsigned) pc * 4u : PTK_OOB;
   }
 
   // Staging is split so that all global loads of a chunk are in flight together: the load phase
-  // only issues loads, the store phase (one chunk later) masks, transforms and writes LDS.
+  // only issues loads, the store phase (one chunk later) transforms and writes LDS.
   float pf[NX][CONV_CK][NJ];
   auto load_chunk = [&](int c0) {
 #pragma unroll
     for (int r = 0; r < CONV_CK; r++) {
-      const unsigned rowo = c0 + r < cin ? (unsigned) (c0 + r) * ldx : 0u;
+      const unsigned rowo = (unsigned) (c0 + r) * ldx4;
 #pragma unroll
       for (int jj = 0; jj < NJ; jj++) {
-        const unsigned o = rowo + pcol[jj];
-        pf[0][r][jj] = xb[o];
+        const unsigned o = voff[jj] + rowo;
+        pf[0][r][jj] = buf_load(rx, o);
         if constexpr (NX == 3) {
-          pf[1][r][jj] = xb1[o];
-          pf[2][r][jj] = xb2[o];
+          pf[1][r][jj] = buf_load(rx1, o);
+          pf[2][r][jj] = buf_load(rx2, o);
         }
       }
     }
   };
-  auto store_chunk = [&](int c0) {
+  auto store_chunk = [&]() {
 #pragma unroll
-    for (int r = 0; r < CONV_CK; r++) {
-      const bool rok = c0 + r < cin;
+    for (int r = 0; r < CONV_CK; r++)
 #pragma unroll
       for (int jj = 0; jj < NJ; jj++) {
         float v;
         if constexpr (NX == 3) v = in_xform<IN>(pf[0][r][jj], pf[1][r][jj], pf[2][r][jj], in_a);
         else v = in_xform<IN>(pf[0][r][jj], 0.0f, 0.0f, in_a);
-        xs[r * XWP + lane + 64 * jj] = (rok & cok[jj]) ? v : 0.0f;
+        xs[r * XWP + lane + 64 * jj] = v;
       }
-    }
   };
 
   f32x16 acc[NB];
@@ -336,62 +359,88 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[nb][v] = 0.0f;
 
-  // A operands: float4 index ((mb*K + k)*nchunk + chunk)*64 + lane
-  const float4 *wa = reinterpret_cast<const float4 *>(d.w) +
-                     ((long long) mb * K * nchunk + chunk0) * 64 + lane;
-  const int wtap = nchunk * 64;   // float4 stride between taps
+  // A operands: float4 ((mb*K + k)*nchunk + chunk)*64 + lane of the relaid weights, read through
+  // a buffer resource based at this wave's first chunk: the lane offset is fixed and the
+  // (tap, chunk) offset is wave-uniform, so a load costs no vector address arithmetic
+  const float4 *wbase = reinterpret_cast<const float4 *>(d.w) + ((long long) mb * K * nchunk + chunk0) * 64;
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      (void *) wbase, (short) 0, (int) ((unsigned) K * (unsigned) nchunk * 1024u), PTK_BUF_WORD3);
+  const unsigned wlane = (unsigned) lane * 16u;
+  const int wtap = nchunk * 1024;  // bytes between taps
+  auto wa = [&](int k, int j) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rw, wlane, k * wtap + j * 1024, 0));
+  };
   constexpr int KA = KT > 0 ? KT : 1;
-  float4 acur[KA];
-  if constexpr (KT > 0) {
-#pragma unroll
-    for (int k = 0; k < KT; k++)
-      if (k < K) acur[k] = wa[k * wtap];
-  }
-  load_chunk(chunk0 * CONV_CK);
   const int lbase = half * XWP + l32 * st - dmin;
-  for (int j = 0; j < nch; j++) {
+
+  auto mfma4 = [&](const float4 a, const float *xr) {
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+      const float *xq = xr + 32 * nb * st;
+      acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, xq[0], acc[nb], 0, 0, 0);
+      acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, xq[2 * XWP], acc[nb], 0, 0, 0);
+      acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, xq[4 * XWP], acc[nb], 0, 0, 0);
+      acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, xq[6 * XWP], acc[nb], 0, 0, 0);
+    }
+  };
+  // one chunk: stage its window (loaded one chunk earlier), start the next chunk's loads, run
+  // the taps.  cur holds this chunk's A operands, nxt receives the next chunk's.
+  auto step = [&](int j, float4 (&cur)[KA], float4 (&nxt)[KA]) {
     __builtin_amdgcn_wave_barrier();
-    store_chunk((chunk0 + j) * CONV_CK);
+    store_chunk();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const bool more = j + 1 < nch;
     if (more) load_chunk((chunk0 + j + 1) * CONV_CK);
     if constexpr (KT > 0) {
+      if (more) {
 #pragma unroll
-      for (int k = 0; k < KT; k++) {
-        if (k < K) {   // predicated, not break: the loop must unroll so acur stays in registers
-          const float4 a = acur[k];
-          if (more) acur[k] = wa[k * wtap + (j + 1) * 64];
-          const float *xr = xs + lbase + k * dil;
-#pragma unroll
-          for (int nb = 0; nb < NB; nb++) {
-            const float *xq = xr + 32 * nb * st;
-            acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, xq[0], acc[nb], 0, 0, 0);
-            acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, xq[2 * XWP], acc[nb], 0, 0, 0);
-            acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, xq[4 * XWP], acc[nb], 0, 0, 0);
-            acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, xq[6 * XWP], acc[nb], 0, 0, 0);
-          }
-        }
+        for (int k = 0; k < KT; k++)
+          if (k < K) nxt[k] = wa(k, j + 1);
       }
+#pragma unroll
+      for (int k = 0; k < KT; k++)
+        if (k < K) mfma4(cur[k], xs + lbase + k * dil);   // predicated: the loop must unroll
     } else {
-      for (int k = 0; k < K; k++) {
-        const float4 a = wa[k * wtap + j * 64];
-        const float *xr = xs + lbase + k * dil;
-#pragma unroll
-        for (int nb = 0; nb < NB; nb++) {
-          const float *xq = xr + 32 * nb * st;
-          acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, xq[0], acc[nb], 0, 0, 0);
-          acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, xq[2 * XWP], acc[nb], 0, 0, 0);
-          acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, xq[4 * XWP], acc[nb], 0, 0, 0);
-          acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, xq[6 * XWP], acc[nb], 0, 0, 0);
-        }
-      }
+      for (int k = 0; k < K; k++) mfma4(wa(k, j), xs + lbase + k * dil);
     }
     __builtin_amdgcn_wave_barrier();
+  };
+
+  float4 a0[KA], a1[KA];
+  if constexpr (KT > 0) {
+#pragma unroll
+    for (int k = 0; k < KT; k++)
+      if (k < K) a0[k] = wa(k, 0);
+  }
+  load_chunk(chunk0 * CONV_CK);
+  for (int j = 0; j < nch; j += 2) {   // two chunks per trip: A ping-pongs between a0 and a1
+    step(j, a0, a1);
+    if (j + 1 < nch) step(j + 1, a1, a0);
   }
 
-  // deterministic cross-wave reduction through LDS: partial sums added in wave order 0..3
+  // epilogue: the S partial sums of a block are added in wave order through LDS, then bias, the
+  // epilogue chain and one store per output
+  const long long qend = d.q0 + d.nq;
+  auto emit = [&](int nb, int v, float sum) {
+    const int m = mb * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+    const long long q = q0 + 32 * nb + l32;
+    if (m >= d.M || q >= qend) return;
+    const int co = m % d.C4, r = m / d.C4;
+    const long long col = q * d.ys + r - d.ypad;
+    if (col < 0 || col >= d.Lout) return;
+    float val = sum + ((d.bias != nullptr && co < d.nbias) ? d.bias[co] : 0.0f);
+    for (int e = 0; e < d.nepi; e++) val = epi_apply(val, d.epi[e], b, co, col);
+    d.y[(long long) b * d.bsy + (long long) co * d.ldy + col] = val;
+  };
+  if (S == 1) {
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) emit(nb, v, acc[nb][v]);
+    return;
+  }
   __syncthreads();
   float *red = smem;
 #pragma unroll
@@ -399,25 +448,14 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
 #pragma unroll
     for (int v = 0; v < 16; v++) red[((w * NB + nb) * 16 + v) * 64 + lane] = acc[nb][v];
   __syncthreads();
-  const long long qend = d.q0 + d.nq;
+  const int nv = 16 / S, v0 = ks * nv, wg0 = cg * S;
 #pragma unroll
   for (int nb = 0; nb < NB; nb++)
-#pragma unroll
-    for (int vv = 0; vv < 4; vv++) {
-      const int v = 4 * w + vv;
-      float s = red[((0 * NB + nb) * 16 + v) * 64 + lane];
-      s += red[((1 * NB + nb) * 16 + v) * 64 + lane];
-      s += red[((2 * NB + nb) * 16 + v) * 64 + lane];
-      s += red[((3 * NB + nb) * 16 + v) * 64 + lane];
-      const int m = mb * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-      const long long q = q0 + 32 * nb + l32;
-      if (m >= d.M || q >= qend) continue;
-      const int co = m % d.C4, r = m / d.C4;
-      const long long col = q * d.ys + r - d.ypad;
-      if (col < 0 || col >= d.Lout) continue;
-      float val = s + ((d.bias != nullptr && co < d.nbias) ? d.bias[co] : 0.0f);
-      for (int e = 0; e < d.nepi; e++) val = epi_apply(val, d.epi[e], b, co, col);
-      d.y[(long long) b * d.bsy + (long long) co * d.ldy + col] = val;
+    for (int vv = 0; vv < nv; vv++) {
+      const int v = v0 + vv;
+      float sum = red[((wg0 * NB + nb) * 16 + v) * 64 + lane];
+      for (int i = 1; i < S; i++) sum += red[(((wg0 + i) * NB + nb) * 16 + v) * 64 + lane];
+      emit(nb, v, sum);
     }
 }
 
@@ -428,12 +466,32 @@ static int conv_window(const ptk_conv_desc *d, int nb) {
 static int win_max(int nb) { return nb == 2 ? WinGeo<2>::XWMAX : WinGeo<1>::XWMAX; }
 static int win_pitch(int nb) { return nb == 2 ? WinGeo<2>::XWP : WinGeo<1>::XWP; }
 
+static int env_knob(const char *name) {
+  const char *e = getenv(name);
+  return e ? atoi(e) : 0;
+}
+
+// channel split: the smallest S in {1, 2, 4} whose grid still gives every SIMD about two waves,
+// else 4 (PTK_CONV_SPLIT overrides)
+static int choose_split(const ptk_conv_desc *const *ds, int n, int nb) {
+  static int env = -1;
+  if (env < 0) env = env_knob("PTK_CONV_SPLIT");
+  if (env == 1 || env == 2 || env == 4) return env;
+  for (int S = 1; S < 4; S *= 2) {
+    const int G = 4 / S;
+    long long waves = 0;
+    for (int i = 0; i < n; i++) {
+      const ptk_conv_desc *d = ds[i];
+      waves += 4LL * ((d->M + 31) / 32) * ((d->nq + 32LL * nb * G - 1) / (32LL * nb * G)) * d->batch;
+    }
+    if (waves >= 2048) return S;
+  }
+  return 4;
+}
+
 static int choose_nb(const ptk_conv_desc *d) {
   static int env_nb = -1;
-  if (env_nb < 0) {
-    const char *e = getenv("PTK_CONV_NB");
-    env_nb = e ? atoi(e) : 0;
-  }
+  if (env_nb < 0) env_nb = env_knob("PTK_CONV_NB");
   if ((env_nb == 1 || env_nb == 2) && conv_window(d, env_nb) <= win_max(env_nb)) return env_nb;
   // two column blocks per wave halve the weight traffic per flop; use them when the grid still
   // has about one workgroup per CU
@@ -447,6 +505,8 @@ extern "C" int ptk_conv_mfma_ok(const ptk_conv_desc *d) {
   if (d->M < 16 || d->cin < 2 || d->K < 1 || d->stride < 1 || d->dil == 0) return 0;
   if (conv_window(d, 1) > win_max(1)) return 0;
   if (d->cinp != ptk_conv_cinp(d->cin)) return 0;
+  // 32-bit buffer offsets: every row offset plus the out-of-range marker must stay below 2^32
+  if ((unsigned long long) d->cinp * (unsigned long long) d->ldx * 4ULL >= 0x80000000ULL) return 0;
   return 1;
 }
 
@@ -492,6 +552,7 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
   const int nb = choose_nb(&dd[order[0]]);
   int kmax = 0, in_op = -1;
   int total = 0;
+  const ptk_conv_desc *live[PTK_MAX_GROUP];
   for (int i = 0; i < ngroup; i++) {
     const ptk_conv_desc *d = &dd[order[i]];
     if (!ptk_conv_mfma_ok(d) || conv_window(d, nb) > win_max(nb)) {
@@ -500,6 +561,10 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
       return -1;
     }
     if (d->nq <= 0 || d->batch <= 0) continue;
+    if (d->in_op != PTK_IN_PLAIN && !(d->in_a >= 0.0f && d->in_a <= 1.0f)) {
+      set_err("ptk_conv_launch: input LeakyReLU slope %g outside [0, 1]", (double) d->in_a);
+      return -1;
+    }
     if (in_op < 0) in_op = d->in_op;
     if (d->in_op != in_op || d->in_op < PTK_IN_PLAIN || d->in_op > PTK_IN_AVG3_LEAKY ||
         (d->in_op == PTK_IN_AVG3_LEAKY && (!d->x1 || !d->x2))) {
@@ -508,11 +573,18 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
     }
     if (d->K > kmax) kmax = d->K;
     g.d[g.ngroup] = *d;
-    g.mt[g.ngroup] = (d->M + 31) / 32;
-    g.nt[g.ngroup] = (int) ((d->nq + 32 * nb - 1) / (32 * nb));
-    g.start[g.ngroup] = total;
-    total += g.mt[g.ngroup] * g.nt[g.ngroup] * d->batch;
+    live[g.ngroup] = d;
     g.ngroup++;
+  }
+  if (g.ngroup == 0) return 0;
+  const int S = choose_split(live, g.ngroup, nb), G = 4 / S;
+  g.split = S;
+  for (int i = 0; i < g.ngroup; i++) {
+    const ptk_conv_desc *d = live[i];
+    g.mt[i] = (d->M + 31) / 32;
+    g.nt[i] = (int) ((d->nq + 32LL * nb * G - 1) / (32LL * nb * G));
+    g.start[i] = total;
+    total += g.mt[i] * g.nt[i] * d->batch;
   }
   for (int i = g.ngroup; i <= PTK_MAX_GROUP; i++) g.start[i] = total;
   if (total == 0) return 0;
