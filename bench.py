@@ -179,7 +179,8 @@ def main():
         f3 = lambda: lib.ptd_mrf(ctx.ptr, model.ptr, stage, x.ptr, T, 0.1, y.ptr)  # noqa: E731
         f3()
         ms = timer.time(f3, 20)
-        cfg[f"config3_mrf{C_}_tflops"] = round(2 * C_ * C_ * T * 3 * 21 / (ms * 1e-3) / 1e12, 3)
+        # 3 dilations x (c1 + c2) x branches K 3 + 7 + 11 = 126 tap-weighted convs of C x C
+        cfg[f"config3_mrf{C_}_tflops"] = round(2 * C_ * C_ * T * 126 / (ms * 1e-3) / 1e12, 3)
         x.free()
         y.free()
     # config 4: one request, one stream
