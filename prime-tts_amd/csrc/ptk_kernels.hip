@@ -383,9 +383,17 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
       acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, xq[6 * XWP], acc[nb], 0, 0, 0);
     }
   };
-  // one chunk: stage its window (loaded one chunk earlier), start the next chunk's loads, run
-  // the taps.  cur holds this chunk's A operands, nxt receives the next chunk's.
-  auto step = [&](int j, float4 (&cur)[KA], float4 (&nxt)[KA]) {
+  // one chunk: stage its window (loaded one chunk earlier), start the next chunk's window loads,
+  // run the taps.  After a tap's four MFMAs have consumed acur[k], the same registers receive that
+  // tap's operands of the next chunk: a prefetch distance of about one chunk, no second buffer.
+  float4 acur[KA];
+  if constexpr (KT > 0) {
+#pragma unroll
+    for (int k = 0; k < KT; k++)
+      if (k < K) acur[k] = wa(k, 0);
+  }
+  load_chunk(chunk0 * CONV_CK);
+  for (int j = 0; j < nch; j++) {
     __builtin_amdgcn_wave_barrier();
     store_chunk();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -394,30 +402,17 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
     const bool more = j + 1 < nch;
     if (more) load_chunk((chunk0 + j + 1) * CONV_CK);
     if constexpr (KT > 0) {
-      if (more) {
 #pragma unroll
-        for (int k = 0; k < KT; k++)
-          if (k < K) nxt[k] = wa(k, j + 1);
+      for (int k = 0; k < KT; k++) {
+        if (k < K) {   // predicated, not break: the loop must unroll so acur stays in registers
+          mfma4(acur[k], xs + lbase + k * dil);
+          if (more) acur[k] = wa(k, j + 1);
+        }
       }
-#pragma unroll
-      for (int k = 0; k < KT; k++)
-        if (k < K) mfma4(cur[k], xs + lbase + k * dil);   // predicated: the loop must unroll
     } else {
       for (int k = 0; k < K; k++) mfma4(wa(k, j), xs + lbase + k * dil);
     }
     __builtin_amdgcn_wave_barrier();
-  };
-
-  float4 a0[KA], a1[KA];
-  if constexpr (KT > 0) {
-#pragma unroll
-    for (int k = 0; k < KT; k++)
-      if (k < K) a0[k] = wa(k, 0);
-  }
-  load_chunk(chunk0 * CONV_CK);
-  for (int j = 0; j < nch; j += 2) {   // two chunks per trip: A ping-pongs between a0 and a1
-    step(j, a0, a1);
-    if (j + 1 < nch) step(j + 1, a1, a0);
   }
 
   // epilogue: the S partial sums of a block are added in wave order through LDS, then bias, the
