@@ -11,6 +11,8 @@
 // applied on the accumulator values right before the single store.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -370,7 +372,6 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   auto wa = [&](int k, int j) {
     return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rw, wlane, k * wtap + j * 1024, 0));
   };
-  constexpr int KA = KT > 0 ? KT : 1;
   const int lbase = half * XWP + l32 * st - dmin;
 
   auto mfma4 = [&](const float4 a, const float *xr) {
@@ -383,36 +384,52 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
       acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, xq[6 * XWP], acc[nb], 0, 0, 0);
     }
   };
-  // one chunk: stage its window (loaded one chunk earlier), start the next chunk's window loads,
-  // run the taps.  After a tap's four MFMAs have consumed acur[k], the same registers receive that
-  // tap's operands of the next chunk: a prefetch distance of about one chunk, no second buffer.
-  float4 acur[KA];
-  if constexpr (KT > 0) {
+  // The chunk loop, for a compile-time tap count KC (0: runtime K, A operands loaded per tap).
+  // Each chunk is straight-line code, so the scheduler can run LDS reads ahead of the MFMAs and
+  // count outstanding loads exactly: stage the window loaded one chunk earlier, issue the next
+  // chunk's window loads, then per tap four MFMAs on acur[k] followed by the load of that tap's
+  // operands for the next chunk into the same registers (prefetch distance about one chunk).  The
+  // last chunk is peeled so it issues no loads.
+  auto run = [&](auto kc) {
+    constexpr int KC = decltype(kc)::value;
+    constexpr int KA = KC > 0 ? KC : 1;
+    float4 acur[KA];
+    auto chunk = [&](int j, auto with_loads) {
+      constexpr bool LD = decltype(with_loads)::value;
+      __builtin_amdgcn_wave_barrier();
+      store_chunk();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if constexpr (LD) load_chunk((chunk0 + j + 1) * CONV_CK);
+      if constexpr (KC > 0) {
 #pragma unroll
-    for (int k = 0; k < KT; k++)
-      if (k < K) acur[k] = wa(k, 0);
-  }
-  load_chunk(chunk0 * CONV_CK);
-  for (int j = 0; j < nch; j++) {
-    __builtin_amdgcn_wave_barrier();
-    store_chunk();
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const bool more = j + 1 < nch;
-    if (more) load_chunk((chunk0 + j + 1) * CONV_CK);
-    if constexpr (KT > 0) {
-#pragma unroll
-      for (int k = 0; k < KT; k++) {
-        if (k < K) {   // predicated, not break: the loop must unroll so acur stays in registers
+        for (int k = 0; k < KC; k++) {
           mfma4(acur[k], xs + lbase + k * dil);
-          if (more) acur[k] = wa(k, j + 1);
+          if constexpr (LD) acur[k] = wa(k, j + 1);
         }
+      } else {
+        for (int k = 0; k < K; k++) mfma4(wa(k, j), xs + lbase + k * dil);
       }
-    } else {
-      for (int k = 0; k < K; k++) mfma4(wa(k, j), xs + lbase + k * dil);
+      __builtin_amdgcn_wave_barrier();
+    };
+    // window loads first, then the A operands: the same order as inside a chunk, so the wait
+    // before the first window store is the same count on entry as on every later trip
+    load_chunk(chunk0 * CONV_CK);
+    if constexpr (KC > 0) {
+#pragma unroll
+      for (int k = 0; k < KC; k++) acur[k] = wa(k, 0);
     }
-    __builtin_amdgcn_wave_barrier();
+    for (int j = 0; j + 1 < nch; j++) chunk(j, std::true_type{});
+    chunk(nch - 1, std::false_type{});
+  };
+  if constexpr (KT > 0) {
+    if (K == KT) run(std::integral_constant<int, KT>{});
+    else if (KT > 7 && K == 7) run(std::integral_constant<int, 7>{});
+    else if (KT > 3 && K == 3) run(std::integral_constant<int, 3>{});
+    else run(std::integral_constant<int, 0>{});
+  } else {
+    run(std::integral_constant<int, 0>{});
   }
 
   // epilogue: the S partial sums of a block are added in wave order through LDS, then bias, the
@@ -469,8 +486,7 @@ static int env_knob(const char *name) {
 // channel split: the smallest S in {1, 2, 4} whose grid still gives every SIMD about two waves,
 // else 4 (PTK_CONV_SPLIT overrides)
 static int choose_split(const ptk_conv_desc *const *ds, int n, int nb) {
-  static int env = -1;
-  if (env < 0) env = env_knob("PTK_CONV_SPLIT");
+  const int env = env_knob("PTK_CONV_SPLIT");
   if (env == 1 || env == 2 || env == 4) return env;
   for (int S = 1; S < 4; S *= 2) {
     const int G = 4 / S;
@@ -485,8 +501,7 @@ static int choose_split(const ptk_conv_desc *const *ds, int n, int nb) {
 }
 
 static int choose_nb(const ptk_conv_desc *d) {
-  static int env_nb = -1;
-  if (env_nb < 0) env_nb = env_knob("PTK_CONV_NB");
+  const int env_nb = env_knob("PTK_CONV_NB");
   if ((env_nb == 1 || env_nb == 2) && conv_window(d, env_nb) <= win_max(env_nb)) return env_nb;
   // two column blocks per wave halve the weight traffic per flop; use them when the grid still
   // has about one workgroup per CU
