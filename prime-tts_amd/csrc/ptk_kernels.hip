@@ -233,22 +233,26 @@ struct ConvGroup {
   int split;                      // waves of a workgroup sharing one output block: 1, 2 or 4
 };
 
-// Staged input window of one channel row: NB column blocks of 32 outputs need
-// (32*NB - 1)*stride + |K-1|*|dil| + 1 columns.  The kernel supports up to 64*(NB+1) columns and
-// lays rows out with pitch 64*(NB+1) + 32: the two 32-lane halves of a wave read rows 2p and 2p+1
-// at the same column, and a pitch = 32 (mod 64) puts them in disjoint bank halves.  The pitch is a
-// compile-time constant so every LDS read of the inner loop is one instruction with an immediate
-// offset.
+// Staged input window of one chunk (8 channels): NB column blocks of 32 outputs need
+// (32*NB - 1)*stride + |K-1|*|dil| + 1 columns; the kernel supports up to 64*(NB+1).  LDS holds it
+// column-major, 8 floats per column ordered [h][p] = channel 2p + h, so the four B operands a lane
+// (column, h) needs for one tap -- channels h, 2+h, 4+h, 6+h -- are one 16-byte LDS read, and the
+// 64 lanes of a wave read 1 KiB of consecutive columns (no bank conflicts at stride 1).
 template <int NB> struct WinGeo {
   static constexpr int NJ = NB + 1;          // 64-column slices a lane loads per row
   static constexpr int XWMAX = 64 * NJ;
-  static constexpr int XWP = XWMAX + 32;
 };
 
 // word 3 of a raw buffer resource on gfx9-family parts (gfx950): 32-bit data, range checked
 #define PTK_BUF_WORD3 0x00020000
 // an offset past every buffer: the load returns 0 (buffer range checking)
 #define PTK_OOB 0x80000000u
+
+// Scheduling fence for global loads: every instruction class except vector-memory may be moved
+// across it (ALU, VALU, SALU, MFMA, LDS).  Placed right after prefetch loads, it keeps the machine
+// scheduler from sinking them towards their use, which it does to shorten register live ranges
+// and which would leave no prefetch distance at all.
+#define PTK_PIN_VMEM() __builtin_amdgcn_sched_barrier(0x0106)
 
 __device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, unsigned off) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
@@ -263,7 +267,7 @@ __device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, unsigned off
 template <int KT, int NB, int IN>
 __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   extern __shared__ float smem[];
-  constexpr int NJ = WinGeo<NB>::NJ, XWP = WinGeo<NB>::XWP;
+  constexpr int NJ = WinGeo<NB>::NJ, XWMAX = WinGeo<NB>::XWMAX;
   constexpr int NX = IN == PTK_IN_AVG3_LEAKY ? 3 : 1;
   int bid = blockIdx.x;
   int p = 0;
@@ -301,7 +305,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   const int XW = (32 * NB - 1) * st + (kd < 0 ? -kd : kd) + 1;
   const long long cmin = q0 * st + dmin - d.shift;
   const int chunk0 = ks * nch;
-  float *xs = smem + w * (CONV_CK * XWP);
+  float4 *xs = reinterpret_cast<float4 *>(smem) + w * (2 * XWMAX);   // [column][h] float4
 
   // Window columns this lane stages, fixed for the wave: byte offset in the row, or an offset the
   // buffer range check turns into 0 (columns outside [0, lim), past the window).  Channels past
@@ -345,14 +349,17 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   };
   auto store_chunk = [&]() {
 #pragma unroll
-    for (int r = 0; r < CONV_CK; r++)
+    for (int jj = 0; jj < NJ; jj++) {
+      float v[CONV_CK];
 #pragma unroll
-      for (int jj = 0; jj < NJ; jj++) {
-        float v;
-        if constexpr (NX == 3) v = in_xform<IN>(pf[0][r][jj], pf[1][r][jj], pf[2][r][jj], in_a);
-        else v = in_xform<IN>(pf[0][r][jj], 0.0f, 0.0f, in_a);
-        xs[r * XWP + lane + 64 * jj] = v;
+      for (int r = 0; r < CONV_CK; r++) {
+        if constexpr (NX == 3) v[r] = in_xform<IN>(pf[0][r][jj], pf[1][r][jj], pf[2][r][jj], in_a);
+        else v[r] = in_xform<IN>(pf[0][r][jj], 0.0f, 0.0f, in_a);
       }
+      float4 *col = xs + 2 * (lane + 64 * jj);
+      col[0] = make_float4(v[0], v[2], v[4], v[6]);
+      col[1] = make_float4(v[1], v[3], v[5], v[7]);
+    }
   };
 
   f32x16 acc[NB];
@@ -372,16 +379,16 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   auto wa = [&](int k, int j) {
     return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rw, wlane, k * wtap + j * 1024, 0));
   };
-  const int lbase = half * XWP + l32 * st - dmin;
+  const int lbase = 2 * (l32 * st - dmin) + half;   // float4 index of tap 0, column block 0
 
-  auto mfma4 = [&](const float4 a, const float *xr) {
+  auto mfma4 = [&](const float4 a, const float4 *xr) {
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) {
-      const float *xq = xr + 32 * nb * st;
-      acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, xq[0], acc[nb], 0, 0, 0);
-      acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, xq[2 * XWP], acc[nb], 0, 0, 0);
-      acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, xq[4 * XWP], acc[nb], 0, 0, 0);
-      acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, xq[6 * XWP], acc[nb], 0, 0, 0);
+      const float4 bq = xr[64 * nb * st];
+      acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, bq.x, acc[nb], 0, 0, 0);
+      acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, bq.y, acc[nb], 0, 0, 0);
+      acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, bq.z, acc[nb], 0, 0, 0);
+      acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, bq.w, acc[nb], 0, 0, 0);
     }
   };
   // The chunk loop, for a compile-time tap count KC (0: runtime K, A operands loaded per tap).
@@ -401,15 +408,21 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      if constexpr (LD) load_chunk((chunk0 + j + 1) * CONV_CK);
+      if constexpr (LD) {
+        load_chunk((chunk0 + j + 1) * CONV_CK);
+        PTK_PIN_VMEM();
+      }
       if constexpr (KC > 0) {
 #pragma unroll
         for (int k = 0; k < KC; k++) {
-          mfma4(acur[k], xs + lbase + k * dil);
-          if constexpr (LD) acur[k] = wa(k, j + 1);
+          mfma4(acur[k], xs + lbase + 2 * k * dil);
+          if constexpr (LD) {
+            acur[k] = wa(k, j + 1);
+            PTK_PIN_VMEM();
+          }
         }
       } else {
-        for (int k = 0; k < K; k++) mfma4(wa(k, j), xs + lbase + k * dil);
+        for (int k = 0; k < K; k++) mfma4(wa(k, j), xs + lbase + 2 * k * dil);
       }
       __builtin_amdgcn_wave_barrier();
     };
@@ -476,7 +489,6 @@ static int conv_window(const ptk_conv_desc *d, int nb) {
   return (32 * nb - 1) * d->stride + (kd < 0 ? -kd : kd) + 1;
 }
 static int win_max(int nb) { return nb == 2 ? WinGeo<2>::XWMAX : WinGeo<1>::XWMAX; }
-static int win_pitch(int nb) { return nb == 2 ? WinGeo<2>::XWP : WinGeo<1>::XWP; }
 
 static int env_knob(const char *name) {
   const char *e = getenv(name);
@@ -500,14 +512,12 @@ static int choose_split(const ptk_conv_desc *const *ds, int n, int nb) {
   return 4;
 }
 
+// column blocks per wave: 1.  Two blocks halve the weight loads per MFMA but double the window
+// registers and halve the grid; on MI355X they lost at every decoder shape measured (batch 1 and
+// 8), so they are only used when PTK_CONV_NB=2 asks for them.
 static int choose_nb(const ptk_conv_desc *d) {
   const int env_nb = env_knob("PTK_CONV_NB");
-  if ((env_nb == 1 || env_nb == 2) && conv_window(d, env_nb) <= win_max(env_nb)) return env_nb;
-  // two column blocks per wave halve the weight traffic per flop; use them when the grid still
-  // has about one workgroup per CU
-  const long long mt = (d->M + 31) / 32;
-  const long long t2 = mt * ((d->nq + 63) / 64) * d->batch;
-  if (t2 >= 224 && conv_window(d, 2) <= win_max(2)) return 2;
+  if (env_nb == 2 && conv_window(d, 2) <= win_max(2)) return 2;
   return 1;
 }
 
@@ -598,7 +608,7 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
   }
   for (int i = g.ngroup; i <= PTK_MAX_GROUP; i++) g.start[i] = total;
   if (total == 0) return 0;
-  const size_t stage = (size_t) CONV_WAVES * CONV_CK * win_pitch(nb) * sizeof(float);
+  const size_t stage = (size_t) CONV_WAVES * CONV_CK * win_max(nb) * sizeof(float);
   const size_t redb = (size_t) CONV_WAVES * 16 * nb * 64 * sizeof(float);
   const size_t lds = stage > redb ? stage : redb;
   hipStream_t s = (hipStream_t) stream;
