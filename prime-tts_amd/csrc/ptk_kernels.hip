@@ -254,8 +254,11 @@ template <int NB> struct WinGeo {
 // and which would leave no prefetch distance at all.
 #define PTK_PIN_VMEM() __builtin_amdgcn_sched_barrier(0x0106)
 
-__device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, unsigned off) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+// voff: per-lane byte offset (PTK_OOB for an element that must read 0); soff: wave-uniform byte
+// offset.  Either placement of the range check (with or without soff) leaves PTK_OOB + soff out of
+// range for the buffers used here, which stay below 2 GiB.
+__device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
 
 // One workgroup = 4 waves.  The waves form 4/S column groups of S waves; the S waves of a group
@@ -308,8 +311,9 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   float4 *xs = reinterpret_cast<float4 *>(smem) + w * (2 * XWMAX);   // [column][h] float4
 
   // Window columns this lane stages, fixed for the wave: byte offset in the row, or an offset the
-  // buffer range check turns into 0 (columns outside [0, lim), past the window).  Channels past
-  // cin fall outside the buffer (num_records = cin rows) and read 0 as well.
+  // buffer range check turns into 0 (columns outside [0, lim), past the window).  The row offset
+  // is wave-uniform and goes into the scalar offset.  A row past cin (zero padding of the last
+  // chunk when cin is not a multiple of 8) reads row 0 and is zeroed when it is stored.
   const long long xoff = (long long) b * d.bsx;
   const unsigned nrec = (unsigned) cin * ldx4;
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
@@ -335,19 +339,19 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   auto load_chunk = [&](int c0) {
 #pragma unroll
     for (int r = 0; r < CONV_CK; r++) {
-      const unsigned rowo = (unsigned) (c0 + r) * ldx4;
+      const unsigned rowo = c0 + r < cin ? (unsigned) (c0 + r) * ldx4 : 0u;
 #pragma unroll
       for (int jj = 0; jj < NJ; jj++) {
-        const unsigned o = voff[jj] + rowo;
-        pf[0][r][jj] = buf_load(rx, o);
+        pf[0][r][jj] = buf_load(rx, voff[jj], rowo);
         if constexpr (NX == 3) {
-          pf[1][r][jj] = buf_load(rx1, o);
-          pf[2][r][jj] = buf_load(rx2, o);
+          pf[1][r][jj] = buf_load(rx1, voff[jj], rowo);
+          pf[2][r][jj] = buf_load(rx2, voff[jj], rowo);
         }
       }
     }
   };
-  auto store_chunk = [&]() {
+  auto store_chunk = [&](int c0) {
+    const int nlive = cin - c0;   // rows of this chunk that hold channels (8 unless cin % 8 != 0)
 #pragma unroll
     for (int jj = 0; jj < NJ; jj++) {
       float v[CONV_CK];
@@ -355,6 +359,10 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
       for (int r = 0; r < CONV_CK; r++) {
         if constexpr (NX == 3) v[r] = in_xform<IN>(pf[0][r][jj], pf[1][r][jj], pf[2][r][jj], in_a);
         else v[r] = in_xform<IN>(pf[0][r][jj], 0.0f, 0.0f, in_a);
+      }
+      if (nlive < CONV_CK) {
+#pragma unroll
+        for (int r = 0; r < CONV_CK; r++) v[r] = r < nlive ? v[r] : 0.0f;
       }
       float4 *col = xs + 2 * (lane + 64 * jj);
       col[0] = make_float4(v[0], v[2], v[4], v[6]);
@@ -404,7 +412,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
     auto chunk = [&](int j, auto with_loads) {
       constexpr bool LD = decltype(with_loads)::value;
       __builtin_amdgcn_wave_barrier();
-      store_chunk();
+      store_chunk((chunk0 + j) * CONV_CK);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -814,9 +822,10 @@ __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, 
   // frames t needed by ola index j = i + 8 >= i_lo + 8: 4t in [j - 15, j]
   const long long t_lo = (i_lo - 4) >> 2;
   __syncthreads();
-  // 1) spectra of the needed frames
-  for (int e = tid; e < 4 * TAIL_NT * 9; e += 256) {
-    const int b = e / (TAIL_NT * 9), rem = e % (TAIL_NT * 9), tt = rem / 9, k = rem % 9;
+  // 1) spectra of the needed frames; consecutive threads take consecutive frames of one
+  //    (band, bin) row, so the reads of p are coalesced
+  for (int e = tid; e < 4 * 9 * TAIL_NT; e += 256) {
+    const int tt = e % TAIL_NT, bk = e / TAIL_NT, b = bk / 9, k = bk % 9;
     const long long t = t_lo + tt;
     float re = 0.0f, im = 0.0f;
     if (t >= 0 && t < L) {
