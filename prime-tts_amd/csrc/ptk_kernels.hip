@@ -235,9 +235,9 @@ struct ConvGroup {
 
 // Staged input window of one chunk (8 channels): NB column blocks of 32 outputs need
 // (32*NB - 1)*stride + |K-1|*|dil| + 1 columns; the kernel supports up to 64*(NB+1).  LDS holds it
-// column-major, 8 floats per column ordered [h][p] = channel 2p + h, so the four B operands a lane
-// (column, h) needs for one tap -- channels h, 2+h, 4+h, 6+h -- are one 16-byte LDS read, and the
-// 64 lanes of a wave read 1 KiB of consecutive columns (no bank conflicts at stride 1).
+// as two planes h = 0, 1 of float4 columns: plane h, column c = channels h, 2+h, 4+h, 6+h.  The
+// four B operands a lane (column, h) needs for one tap are then one 16-byte LDS read, and each
+// half-wave reads (and each staging store writes) consecutive 16-byte columns: no bank conflicts.
 template <int NB> struct WinGeo {
   static constexpr int NJ = NB + 1;          // 64-column slices a lane loads per row
   static constexpr int XWMAX = 64 * NJ;
@@ -308,7 +308,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   const int XW = (32 * NB - 1) * st + (kd < 0 ? -kd : kd) + 1;
   const long long cmin = q0 * st + dmin - d.shift;
   const int chunk0 = ks * nch;
-  float4 *xs = reinterpret_cast<float4 *>(smem) + w * (2 * XWMAX);   // [column][h] float4
+  float4 *xs = reinterpret_cast<float4 *>(smem) + w * (2 * XWMAX);   // [h][column] float4
 
   // Window columns this lane stages, fixed for the wave: byte offset in the row, or an offset the
   // buffer range check turns into 0 (columns outside [0, lim), past the window).  The row offset
@@ -364,9 +364,8 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
 #pragma unroll
         for (int r = 0; r < CONV_CK; r++) v[r] = r < nlive ? v[r] : 0.0f;
       }
-      float4 *col = xs + 2 * (lane + 64 * jj);
-      col[0] = make_float4(v[0], v[2], v[4], v[6]);
-      col[1] = make_float4(v[1], v[3], v[5], v[7]);
+      xs[lane + 64 * jj] = make_float4(v[0], v[2], v[4], v[6]);
+      xs[XWMAX + lane + 64 * jj] = make_float4(v[1], v[3], v[5], v[7]);
     }
   };
 
@@ -387,12 +386,12 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   auto wa = [&](int k, int j) {
     return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rw, wlane, k * wtap + j * 1024, 0));
   };
-  const int lbase = 2 * (l32 * st - dmin) + half;   // float4 index of tap 0, column block 0
+  const int lbase = half * XWMAX + l32 * st - dmin;   // float4 index of tap 0, column block 0
 
   auto mfma4 = [&](const float4 a, const float4 *xr) {
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) {
-      const float4 bq = xr[64 * nb * st];
+      const float4 bq = xr[32 * nb * st];
       acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, bq.x, acc[nb], 0, 0, 0);
       acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, bq.y, acc[nb], 0, 0, 0);
       acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, bq.z, acc[nb], 0, 0, 0);
@@ -423,14 +422,14 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
       if constexpr (KC > 0) {
 #pragma unroll
         for (int k = 0; k < KC; k++) {
-          mfma4(acur[k], xs + lbase + 2 * k * dil);
+          mfma4(acur[k], xs + lbase + k * dil);
           if constexpr (LD) {
             acur[k] = wa(k, j + 1);
             PTK_PIN_VMEM();
           }
         }
       } else {
-        for (int k = 0; k < K; k++) mfma4(wa(k, j), xs + lbase + 2 * k * dil);
+        for (int k = 0; k < K; k++) mfma4(wa(k, j), xs + lbase + k * dil);
       }
       __builtin_amdgcn_wave_barrier();
     };
