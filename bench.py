@@ -70,13 +70,17 @@ class EventTimer:
 
 
 def mrf_depth_setup(pkg, ctx, stage, T):
+    """Inputs of one MRF residual unit as the decoder hands them over: the branch inputs and their
+    LeakyReLU(0.1) copies (written by the producing conv's epilogue in the decoder)."""
     C_ = 256 if stage == 0 else 128
     rng = np.random.default_rng(77)
-    xs = [pkg.DevBuf.of(ctx, rng.standard_normal((C_, T)).astype(np.float32)) for _ in range(3)]
+    xr = [rng.standard_normal((C_, T)).astype(np.float32) for _ in range(3)]
+    xs = [pkg.DevBuf.of(ctx, x) for x in xr]
+    xls = [pkg.DevBuf.of(ctx, np.where(x >= 0, x, np.float32(0.1) * x).astype(np.float32)) for x in xr]
     a_s = [pkg.DevBuf(C_ * T) for _ in range(3)]
     ys = [pkg.DevBuf(C_ * T) for _ in range(3)]
     arr = lambda bufs: (C.c_void_p * 3)(*[b.ptr for b in bufs])  # noqa: E731
-    return xs + a_s + ys, arr(xs), arr(a_s), arr(ys)
+    return xs + xls + a_s + ys, arr(xs), arr(xls), arr(a_s), arr(ys)
 
 
 def cpu_baseline(pkg):
@@ -130,8 +134,8 @@ def main():
     # ---------------------------------------------------------------- dominant kernel
     # one MRF-256 depth at config 3 (C=256, T=904): two grouped conv launches of 3 branches each
     flop_launch = 2.0 * 256 * 256 * 904 * (3 + 7 + 11)
-    bufs, xin, a_s, ys = mrf_depth_setup(pkg, ctx, 0, 904)
-    run_depth = lambda: lib.ptd_mrf_depth(ctx.ptr, model.ptr, 0, 2, xin, a_s, ys, 904)  # noqa: E731
+    bufs, xin, xinl, a_s, ys = mrf_depth_setup(pkg, ctx, 0, 904)
+    run_depth = lambda: lib.ptd_mrf_depth(ctx.ptr, model.ptr, 0, 2, xin, xinl, a_s, ys, None, 904)  # noqa: E731
     if args.kernel_loop:
         for _ in range(args.kernel_loop):
             if run_depth() != 0:

@@ -64,11 +64,14 @@ int ptd_mrf(pt_ctx *c, const ptd_model *m, int stage, const float *x, int64_t T,
             float *out);
 
 /* One depth j (0..2, dilation 1/3/5) of an MRF stack: the three branches' c1 convs in one
- * grouped launch (input xin[br] staged through LeakyReLU(0.1), epilogue LeakyReLU(0.1) -> a[br]),
- * then their c2 convs in one grouped launch (epilogue adds the residual xin[br] -> y[br]).  All
- * [C][T].  Asynchronous.  Two kernel launches of 2*C*C*T*(3+7+11) flops each. */
+ * grouped launch (input LeakyReLU(0.1)(xin[br]): read from xin_leaky[br] when given, else applied
+ * to xin[br] as it is staged; epilogue LeakyReLU(0.1) -> a[br]), then their c2 convs in one
+ * grouped launch (epilogue adds the residual xin[br] -> y[br], and writes LeakyReLU(0.1) of it to
+ * y_leaky[br] when y_leaky is given).  All [C][T].  Asynchronous.  Two kernel launches of
+ * 2*C*C*T*(3+7+11) flops each. */
 int ptd_mrf_depth(pt_ctx *c, const ptd_model *m, int stage, int depth, const float *const *xin,
-                  float *const *a, float *const *y, int64_t T);
+                  const float *const *xin_leaky, float *const *a, float *const *y,
+                  float *const *y_leaky, int64_t T);
 
 /* Long-form request through overlap-save windows (config 5; the reference's streaming driver,
  * main_v21_serve.c:210-264 with pt_v21_host.c:2749-2912): frames [a - ctx, a + hop + ctx) are

@@ -3,9 +3,11 @@
  * Graph (ref/v21_graph_trace.txt:3819-4065), with every host op of the reference fused:
  *   conv_pre 192->512 K7 + LeakyReLU(0.1)          one conv, epilogue leaky
  *   ups.0 convT 512->256 K16 s4 p6                  one phase-form GEMM (4 phases = 1024 rows)
- *   MRF-256: per depth j, one grouped launch of the three branches' c1 (LeakyReLU(0.1) applied
- *            to the input as it is staged, epilogue leaky), then one of their c2 (epilogue adds
- *            the residual)  -> 6 launches, three branch outputs left in HBM
+ *   MRF-256: per depth j, one grouped launch of the three branches' c1 (input already
+ *            LeakyReLU'd by its producer, epilogue leaky), then one of their c2 (epilogue adds the
+ *            residual and, for depths 0 and 1, also writes the LeakyReLU'd copy the next depth's
+ *            c1 reads)  -> 6 launches, three branch outputs left in HBM.  ups.0 / ups.1 write
+ *            their output and its LeakyReLU'd copy the same way.
  *   ups.1 convT 256->128: input staged as leaky(((b0 + b1) + b2) / 3, 0.1)
  *   MRF-128 as above
  *   conv_post 128->72 K7: input staged as leaky((...)/3, 0.01) through the (1, 0) reflection pad
@@ -176,19 +178,28 @@ static void epi_push(ptk_conv_desc *d, int op, float a, const float *t, int64_t 
   d->nepi++;
 }
 
-/* one MRF depth for `batch` items: c1 group then c2 group (see ptd_mrf_depth) */
+/* One MRF depth for `batch` items: c1 group then c2 group (see ptd_mrf_depth).  xinL[br]: the
+ * LeakyReLU(0.1)'d input of branch br, or NULL to apply the LeakyReLU while staging xin[br];
+ * yL: when not NULL, c2 also writes LeakyReLU(0.1) of its output there. */
 static int mrf_depth(pt_ctx *c, const ptd_model *m, int stage, int j, const float *const *xin,
-                     float *const *a, float *const *y, int64_t T, int batch) {
+                     const float *const *xinL, float *const *a, float *const *y,
+                     float *const *yL, int64_t T, int batch) {
   const int base = stage == 0 ? 2 : 21, C = stage == 0 ? 256 : 128;
   ptk_conv_desc d1[3], d2[3];
   for (int br = 0; br < 3; br++) {
     const int i1 = base + br * 6 + j * 2, i2 = i1 + 1;
-    conv_layer_desc(&d1[br], m, i1, xin[br], T, T, batch, a[br], T);
-    d1[br].in_op = PTK_IN_LEAKY;
-    d1[br].in_a = 0.1f;
+    conv_layer_desc(&d1[br], m, i1, xinL ? xinL[br] : xin[br], T, T, batch, a[br], T);
+    if (!xinL) {
+      d1[br].in_op = PTK_IN_LEAKY;
+      d1[br].in_a = 0.1f;
+    }
     epi_push(&d1[br], PTK_EPI_LEAKY, 0.1f, NULL, 0, 0);
     conv_layer_desc(&d2[br], m, i2, a[br], T, T, batch, y[br], T);
     epi_push(&d2[br], PTK_EPI_ADDT, 0.0f, xin[br], T, (int64_t) C * T);
+    if (yL) {
+      d2[br].y2 = yL[br];
+      d2[br].a2 = 0.1f;
+    }
   }
   if (ptk_conv_launch(d1, 3, c->g_stream) || ptk_conv_launch(d2, 3, c->g_stream)) {
     PT_LOG("MRF depth %d failed: %s", j, ptk_last_error());
@@ -198,44 +209,47 @@ static int mrf_depth(pt_ctx *c, const ptd_model *m, int stage, int j, const floa
 }
 
 int ptd_mrf_depth(pt_ctx *c, const ptd_model *m, int stage, int depth, const float *const *xin,
-                  float *const *a, float *const *y, int64_t T) {
+                  const float *const *xin_leaky, float *const *a, float *const *y,
+                  float *const *y_leaky, int64_t T) {
   if (!c || !c->use_cuda || !m || (stage != 0 && stage != 1) || depth < 0 || depth > 2 || T < 1)
     return -1;
-  return mrf_depth(c, m, stage, depth, xin, a, y, T, 1);
+  return mrf_depth(c, m, stage, depth, xin, xin_leaky, a, y, y_leaky, T, 1);
 }
 
-/* MRF stack on x [batch][C][T]: writes the three branch outputs (before the average) */
-static int mrf_run(pt_ctx *c, const ptd_model *m, int stage, const float *x, int64_t T, int batch,
-                   float *const out[3]) {
+/* MRF stack on x [batch][C][T] (xL = LeakyReLU(0.1)(x), or NULL): writes the three branch
+ * outputs (before the average) */
+static int mrf_run(pt_ctx *c, const ptd_model *m, int stage, const float *x, const float *xL,
+                   int64_t T, int batch, float *const out[3]) {
   const int C = stage == 0 ? 256 : 128;
   const size_t tb = (size_t) batch * C * T * sizeof(float);
-  float *a[3], *yb[3];
+  float *a[3], *yb[3], *lb[3];
   for (int br = 0; br < 3; br++) {
     a[br] = ptdi_arena_alloc(c, tb);
     yb[br] = ptdi_arena_alloc(c, tb);
-    if (!a[br] || !yb[br]) {
+    lb[br] = ptdi_arena_alloc(c, tb);
+    if (!a[br] || !yb[br] || !lb[br]) {
       PT_LOG("arena too small for the MRF stack (T %lld batch %d)", (long long) T, batch);
       return -1;
     }
   }
-  /* ping-pong: depth 0 writes out[], 1 writes yb[], 2 writes out[] again */
-  const float *prev[3] = {x, x, x};
-  for (int j = 0; j < 3; j++) {
-    float *cur[3];
-    for (int br = 0; br < 3; br++) cur[br] = (j == 1) ? yb[br] : out[br];
-    if (mrf_depth(c, m, stage, j, prev, a, cur, T, batch)) return -1;
-    for (int br = 0; br < 3; br++) prev[br] = cur[br];
-  }
-  return 0;
+  /* depth 0: x -> out[] (+ lb[]); depth 1: out[] -> yb[] (+ lb[], rewritten after depth 1's c1
+   * has read it: same stream); depth 2: yb[] -> out[] */
+  const float *xs[3] = {x, x, x}, *xls[3] = {xL, xL, xL};
+  if (mrf_depth(c, m, stage, 0, xs, xL ? xls : NULL, a, out, lb, T, batch)) return -1;
+  const float *p1[3] = {out[0], out[1], out[2]}, *l1[3] = {lb[0], lb[1], lb[2]};
+  if (mrf_depth(c, m, stage, 1, p1, l1, a, yb, lb, T, batch)) return -1;
+  const float *p2[3] = {yb[0], yb[1], yb[2]};
+  return mrf_depth(c, m, stage, 2, p2, l1, a, out, NULL, T, batch);
 }
 
 size_t ptd_decode_arena_bytes(int64_t T, int batch) {
   const size_t f = sizeof(float) * (size_t) batch;
   const int64_t T1 = 4 * T, T2 = 16 * T, L = T2 + 1;
   size_t s = 0;
-  s += al256(f * 512 * T) + al256(f * 256 * T1) + 3 * al256(f * 256 * T1);   /* h, x0, o[] */
-  size_t mrf0 = 6 * al256(f * 256 * T1);
-  size_t late = al256(f * 128 * T2) + 3 * al256(f * 128 * T2) + 6 * al256(f * 128 * T2) + al256(f * 72 * L);
+  s += al256(f * 512 * T) + 2 * al256(f * 256 * T1) + 3 * al256(f * 256 * T1);   /* h, x0, x0L, o[] */
+  size_t mrf0 = 9 * al256(f * 256 * T1);
+  size_t late = 2 * al256(f * 128 * T2) + 3 * al256(f * 128 * T2) + 9 * al256(f * 128 * T2) +
+                al256(f * 72 * L);
   return s + (mrf0 > late ? mrf0 : late) + 4096;
 }
 
@@ -248,9 +262,10 @@ static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t T,
   int rc = -1;
   float *h = ptdi_arena_alloc(c, f * 512 * T);
   float *x0 = ptdi_arena_alloc(c, f * 256 * T1);
+  float *x0L = ptdi_arena_alloc(c, f * 256 * T1);
   float *o0[3] = {ptdi_arena_alloc(c, f * 256 * T1), ptdi_arena_alloc(c, f * 256 * T1),
                   ptdi_arena_alloc(c, f * 256 * T1)};
-  if (!h || !x0 || !o0[0] || !o0[1] || !o0[2]) goto oom;
+  if (!h || !x0 || !x0L || !o0[0] || !o0[1] || !o0[2]) goto oom;
   ptk_conv_desc d;
   /* conv_pre + LeakyReLU */
   conv_layer_desc(&d, m, 0, z, T, T, batch, h, T);
@@ -258,14 +273,17 @@ static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t T,
   if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
   /* ups.0 */
   ptdi_convT_desc(&d, h, T, 512 * T, T, 512, m->wr[1], m->b[1], 256, 4, 6, 16, x0, T1, 256 * T1, batch);
+  d.y2 = x0L;
+  d.a2 = 0.1f;
   if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
   void *mark1 = ptdi_arena_mark(c);
-  if (mrf_run(c, m, 0, x0, T1, batch, o0)) goto fail;
+  if (mrf_run(c, m, 0, x0, x0L, T1, batch, o0)) goto fail;
   ptdi_arena_release(c, mark1);   /* the MRF temporaries; o0[] stay */
   float *x1 = ptdi_arena_alloc(c, f * 128 * T2);
+  float *x1L = ptdi_arena_alloc(c, f * 128 * T2);
   float *o1[3] = {ptdi_arena_alloc(c, f * 128 * T2), ptdi_arena_alloc(c, f * 128 * T2),
                   ptdi_arena_alloc(c, f * 128 * T2)};
-  if (!x1 || !o1[0] || !o1[1] || !o1[2]) goto oom;
+  if (!x1 || !x1L || !o1[0] || !o1[1] || !o1[2]) goto oom;
   /* ups.1 over leaky(avg(branches), 0.1) */
   ptdi_convT_desc(&d, o0[0], T1, 256 * T1, T1, 256, m->wr[20], m->b[20], 128, 4, 6, 16, x1, T2,
                   128 * T2, batch);
@@ -273,9 +291,11 @@ static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t T,
   d.x2 = o0[2];
   d.in_op = PTK_IN_AVG3_LEAKY;
   d.in_a = 0.1f;
+  d.y2 = x1L;
+  d.a2 = 0.1f;
   if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
   void *mark2 = ptdi_arena_mark(c);
-  if (mrf_run(c, m, 1, x1, T2, batch, o1)) goto fail;
+  if (mrf_run(c, m, 1, x1, x1L, T2, batch, o1)) goto fail;
   ptdi_arena_release(c, mark2);
   float *p = ptdi_arena_alloc(c, f * 72 * L);
   if (!p) goto oom;
@@ -354,7 +374,7 @@ int ptd_mrf(pt_ctx *c, const ptd_model *m, int stage, const float *x, int64_t T,
   void *mark = ptdi_arena_mark(c);
   float *o[3] = {ptdi_arena_alloc(c, tb), ptdi_arena_alloc(c, tb), ptdi_arena_alloc(c, tb)};
   int rc = -1;
-  if (o[0] && o[1] && o[2] && !mrf_run(c, m, stage, x, T, 1, o) &&
+  if (o[0] && o[1] && o[2] && !mrf_run(c, m, stage, x, NULL, T, 1, o) &&
       !ptk_avg3_leaky(o[0], o[1], o[2], out, (int64_t) C * T, alpha, c->g_stream))
     rc = 0;
   else

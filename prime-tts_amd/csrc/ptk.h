@@ -89,6 +89,9 @@ typedef struct {
   int64_t q0, nq;             /* output columns [q0, q0 + nq) */
   /* output */
   float *y;
+  float *y2;                  /* optional second output: LeakyReLU(a2) of every value stored in y,
+                                 same index (the next conv's pre-activated input) */
+  float a2;
   int64_t ldy, bsy;
   int ys, ypad;
   int64_t Lout;

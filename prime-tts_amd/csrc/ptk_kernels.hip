@@ -464,7 +464,9 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
     if (col < 0 || col >= d.Lout) return;
     float val = sum + ((d.bias != nullptr && co < d.nbias) ? d.bias[co] : 0.0f);
     for (int e = 0; e < d.nepi; e++) val = epi_apply(val, d.epi[e], b, co, col);
-    d.y[(long long) b * d.bsy + (long long) co * d.ldy + col] = val;
+    const long long yi = (long long) b * d.bsy + (long long) co * d.ldy + col;
+    d.y[yi] = val;
+    if (d.y2 != nullptr) d.y2[yi] = val >= 0.0f ? val : d.a2 * val;
   };
   if (S == 1) {
 #pragma unroll
