@@ -253,8 +253,13 @@ size_t ptd_decode_arena_bytes(int64_t T, int batch) {
   return s + (mrf0 > late ? mrf0 : late) + 4096;
 }
 
-static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int batch,
-                       float *wav, float *const *stages) {
+/* Decode `batch` items of T frames.  Item b's latents are z + b*bsz with rows ldz apart (a plain
+ * batch: ldz = T, bsz = 192*T; overlap-save windows read the sequence in place: ldz = the sequence
+ * length, bsz = the window hop).  Item b's waveform goes to wav + b*bsw; only the samples `emit`
+ * names are stored (NULL: all). */
+static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t ldz, int64_t bsz,
+                       int64_t T, int batch, float *wav, int64_t bsw, const ptk_emit *emit,
+                       float *const *stages) {
   if (!c || !c->use_cuda || !m || !z || !wav || T < 1 || batch < 1) return -1;
   const int64_t T1 = 4 * T, T2 = 16 * T, L = T2 + 1;
   const size_t f = sizeof(float) * (size_t) batch;
@@ -268,7 +273,8 @@ static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t T,
   if (!h || !x0 || !x0L || !o0[0] || !o0[1] || !o0[2]) goto oom;
   ptk_conv_desc d;
   /* conv_pre + LeakyReLU */
-  conv_layer_desc(&d, m, 0, z, T, T, batch, h, T);
+  ptdi_conv_desc(&d, z, ldz, bsz, T, 192, m->wr[0], m->b[0], 512, 7, 1, 1, 3, 512, h, T, 512 * T, T,
+                 batch);
   epi_push(&d, PTK_EPI_LEAKY, 0.1f, NULL, 0, 0);
   if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
   /* ups.0 */
@@ -308,7 +314,7 @@ static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t T,
   d.in_a = 0.01f;
   d.reflect_l1 = 1;
   if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
-  if (ptk_tail_batched(p, L, 72 * L, L, wav, 256 * T, batch, m->consts, c->g_stream)) goto fail;
+  if (ptk_tail_batched(p, L, 72 * L, L, wav, bsw, batch, m->consts, emit, c->g_stream)) goto fail;
   if (stages) {
     const size_t fl = sizeof(float);
     if ((stages[0] && ptk_d2d_async(stages[0], h, fl * 512 * T, c->g_stream)) ||
@@ -333,12 +339,12 @@ done:
 }
 
 int ptd_decode(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int batch, float *wav) {
-  return decode_impl(c, m, z, T, batch, wav, NULL);
+  return decode_impl(c, m, z, T, 192 * T, T, batch, wav, 256 * T, NULL, NULL);
 }
 
 int ptd_decode_stages(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, float *wav,
                       float *const *stages) {
-  return decode_impl(c, m, z, T, 1, wav, stages);
+  return decode_impl(c, m, z, T, 192 * T, T, 1, wav, 256 * T, NULL, stages);
 }
 
 int ptd_layer(pt_ctx *c, const ptd_model *m, int layer, const float *x, int64_t T, int batch,
@@ -418,6 +424,10 @@ static int win_schedule(int64_t T, int win, int ctx, win_t *out, int cap) {
 
 #define MAX_WIN 4096
 
+/* The windows of one sequence: the full-width ones start at a = i*hop (hop = win - 2*ctx) and run
+ * as one batched decode that reads z in place (batch stride hop) and writes each window's kept
+ * frames straight to their place in wav (item stride hop*256); a shorter last window runs as a
+ * second decode.  No copies. */
 size_t ptd_windows_arena_bytes(int64_t T, int win, int ctx) {
   win_t *w = malloc(sizeof(win_t) * MAX_WIN);
   if (!w) return 0;
@@ -426,14 +436,11 @@ size_t ptd_windows_arena_bytes(int64_t T, int win, int ctx) {
   size_t tail = 0;
   for (int i = 0; i < n; i++) {
     if (w[i].w == win) nfull++;
-    else tail = ptd_decode_arena_bytes(w[i].w, 1) + al256(sizeof(float) * 256 * w[i].w) +
-                al256(sizeof(float) * 192 * w[i].w);
+    else tail = ptd_decode_arena_bytes(w[i].w, 1);
   }
   free(w);
-  size_t full = nfull ? ptd_decode_arena_bytes(win, nfull) + al256(sizeof(float) * nfull * 192 * win) +
-                            al256(sizeof(float) * nfull * 256 * win)
-                      : 0;
-  return full + tail + 4096;
+  const size_t full = nfull ? ptd_decode_arena_bytes(win, nfull) : 0;
+  return (full > tail ? full : tail) + 4096;
 }
 
 int ptd_decode_windows(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int win, int ctx,
@@ -442,55 +449,31 @@ int ptd_decode_windows(pt_ctx *c, const ptd_model *m, const float *z, int64_t T,
   win_t *ws = malloc(sizeof(win_t) * MAX_WIN);
   if (!ws) return -1;
   const int n = win_schedule(T, win, ctx, ws, MAX_WIN);
-  void *mark = ptdi_arena_mark(c);
-  int rc = -1, nfull = 0;
-  for (int i = 0; i < n; i++) nfull += ws[i].w == win;
-  const size_t fl = sizeof(float);
+  const int64_t hop = win - 2 * ctx;
+  int rc = 0, nfull = 0;
+  while (nfull < n && ws[nfull].w == win) nfull++;
+  /* the schedule's invariants this relies on: full windows first, evenly spaced, kept frames
+   * [a + (i ? ctx : 0), a + win - ctx) except a full last window, which keeps up to a + win */
+  for (int i = 0; i < nfull; i++) {
+    const int64_t lo = i ? ctx : 0, hi = (i + 1 == n) ? win : win - ctx;
+    if (ws[i].a != i * hop || ws[i].e0 != ws[i].a + lo || ws[i].e1 != ws[i].a + hi) rc = -1;
+  }
+  if (rc || nfull + 1 < n) {
+    PT_LOG("windowed decode: unexpected window schedule (T %lld win %d ctx %d)", (long long) T, win, ctx);
+    free(ws);
+    return -1;
+  }
   if (nfull) {
-    float *zb = ptdi_arena_alloc(c, fl * nfull * 192 * win);
-    float *wb = ptdi_arena_alloc(c, fl * nfull * 256 * win);
-    if (!zb || !wb) goto oom;
-    int k = 0;
-    for (int i = 0; i < n; i++) {
-      if (ws[i].w != win) continue;
-      if (ptk_d2d_2d_async(zb + (size_t) k * 192 * win, fl * win, z + ws[i].a, fl * T, fl * win, 192,
-                           c->g_stream))
-        goto fail;
-      k++;
-    }
-    if (decode_impl(c, m, zb, win, nfull, wb, NULL)) goto fail;
-    k = 0;
-    for (int i = 0; i < n; i++) {
-      if (ws[i].w != win) continue;
-      const int64_t cnt = (ws[i].e1 - ws[i].e0) * 256, skip = (ws[i].e0 - ws[i].a) * 256;
-      if (cnt > 0 && ptk_d2d_async(wav + ws[i].e0 * 256, wb + (size_t) k * 256 * win + skip,
-                                   fl * (size_t) cnt, c->g_stream))
-        goto fail;
-      k++;
-    }
+    const ptk_emit em = {0, (int64_t) ctx * 256, (int64_t) (win - ctx) * 256,
+                         (int64_t) (nfull == n ? win : win - ctx) * 256};
+    rc = decode_impl(c, m, z, T, hop, win, nfull, wav, hop * 256, &em, NULL);
   }
-  for (int i = 0; i < n; i++) {
-    if (ws[i].w == win) continue;
-    const int64_t w = ws[i].w;
-    float *zb = ptdi_arena_alloc(c, fl * 192 * w), *wb = ptdi_arena_alloc(c, fl * 256 * w);
-    if (!zb || !wb) goto oom;
-    if (ptk_d2d_2d_async(zb, fl * w, z + ws[i].a, fl * T, fl * w, 192, c->g_stream) ||
-        decode_impl(c, m, zb, w, 1, wb, NULL))
-      goto fail;
-    const int64_t cnt = (ws[i].e1 - ws[i].e0) * 256, skip = (ws[i].e0 - ws[i].a) * 256;
-    if (cnt > 0 && ptk_d2d_async(wav + ws[i].e0 * 256, wb + skip, fl * (size_t) cnt, c->g_stream))
-      goto fail;
+  if (rc == 0 && nfull < n) {   /* the shorter last window */
+    const win_t *l = &ws[n - 1];
+    const ptk_emit em = {(l->e0 - l->a) * 256, 0, (l->e1 - l->a) * 256, (l->e1 - l->a) * 256};
+    rc = decode_impl(c, m, z + l->a, T, 0, l->w, 1, wav + l->a * 256, 0, &em, NULL);
   }
-  rc = 0;
-  goto done;
-oom:
-  PT_LOG("arena too small for windowed decode of T %lld (need %zu MiB)", (long long) T,
-         ptd_windows_arena_bytes(T, win, ctx) >> 20);
-  goto done;
-fail:
-  PT_LOG("windowed decode failed: %s", ptk_last_error());
-done:
-  ptdi_arena_release(c, mark);
+  if (rc) PT_LOG("windowed decode failed: %s", ptk_last_error());
   free(ws);
   return rc;
 }

@@ -136,9 +136,15 @@ int ptk_avg3_leaky(const float *a, const float *b, const float *c, float *y, int
 
 /* decoder tail: conv_post output p [72][L] (row stride ldp) -> wav [16*(L-1)] (iSTFT + PQMF) */
 int ptk_tail(const float *p, int64_t ldp, int64_t L, float *wav, const float *consts, void *s);
+/* which samples of each batch item are stored: item i keeps local samples [lo_i, hi_i) with
+ * lo_i = lo_first for i == 0 else lo, hi_i = hi_last for the last item else hi (overlap-save
+ * windows keep only their interior); the rest is computed and dropped */
+typedef struct {
+  int64_t lo_first, lo, hi, hi_last;
+} ptk_emit;
 /* batched: item b reads p + b*bsp and writes wav + b*bsw */
 int ptk_tail_batched(const float *p, int64_t ldp, int64_t bsp, int64_t L, float *wav, int64_t bsw,
-                     int batch, const float *consts, void *s);
+                     int batch, const float *consts, const ptk_emit *emit, void *s);
 /* the tail's constant table (floats): hann[16], basis_c[9*16], basis_s[9*16], pqmf[4*63] */
 #define PTK_TAIL_NCONST (16 + 144 + 144 + 252)
 

@@ -804,7 +804,11 @@ extern "C" int ptk_leaky(const float *a, float *y, int64_t n, float alpha, void 
 __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, long long ldp,
                                                     long long bsp, long long L,
                                                     float *__restrict__ wav, long long bsw,
-                                                    const float *__restrict__ cst) {
+                                                    const float *__restrict__ cst, ptk_emit em) {
+  // samples of this item that are kept; a block entirely outside them does no work
+  const long long e_lo = blockIdx.y == 0 ? em.lo_first : em.lo;
+  const long long e_hi = blockIdx.y + 1 == gridDim.y ? em.hi_last : em.hi;
+  if ((long long) blockIdx.x * TAIL_OUT >= e_hi || ((long long) blockIdx.x + 1) * TAIL_OUT <= e_lo) return;
   __shared__ float s_c[PTK_TAIL_NCONST];
   __shared__ float s_re[4][TAIL_NT][9], s_im[4][TAIL_NT][9];
   __shared__ float s_fr[4][TAIL_NT][16];
@@ -886,26 +890,29 @@ __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, 
       acc += h[b * 63 + m] * (4.0f * s_y[b][(int) (i - i_lo)]);
     }
   }
-  wav[o] = acc;
+  if (o >= e_lo && o < e_hi) wav[o] = acc;
 }
 
 extern "C" int ptk_tail_batched(const float *p, int64_t ldp, int64_t bsp, int64_t L, float *wav,
-                                int64_t bsw, int batch, const float *consts, void *s) {
+                                int64_t bsw, int batch, const float *consts, const ptk_emit *emit,
+                                void *s) {
   if (L < 2) {
     set_err("ptk_tail: need at least 2 frames (got %lld)", (long long) L);
     return -1;
   }
   if (batch <= 0) return 0;
   const long long nout = 16 * (L - 1);
+  const ptk_emit all = {0, 0, nout, nout};
+  const ptk_emit em = emit ? *emit : all;
   const unsigned blocks = (unsigned) ((nout + TAIL_OUT - 1) / TAIL_OUT);
   hipLaunchKernelGGL(tail_kernel, dim3(blocks, (unsigned) batch), dim3(256), 0, (hipStream_t) s, p,
-                     (long long) ldp, (long long) bsp, (long long) L, wav, (long long) bsw, consts);
+                     (long long) ldp, (long long) bsp, (long long) L, wav, (long long) bsw, consts, em);
   HCHK(hipGetLastError());
   return 0;
 }
 extern "C" int ptk_tail(const float *p, int64_t ldp, int64_t L, float *wav, const float *consts,
                         void *s) {
-  return ptk_tail_batched(p, ldp, 0, L, wav, 0, 1, consts, s);
+  return ptk_tail_batched(p, ldp, 0, L, wav, 0, 1, consts, NULL, s);
 }
 
 // ------------------------------------------------------------------------------ MFMA layout probe

@@ -196,6 +196,38 @@ def test_windows_small_vs_oracle(env):
     dz.free(); dw.free()
 
 
+@pytest.mark.parametrize("T,win,cx", [(20, 32, 8), (32, 32, 8), (48, 32, 8), (57, 32, 8), (70, 32, 8),
+                                      (100, 40, 4)])
+def test_windows_schedule_edges_bitexact(env, T, win, cx):
+    """The windowed decode (one batched decode reading the latents in place, each window's kept
+    frames written straight to the output) equals per-window single decodes stitched by the
+    reference's schedule (main_v21_serve.c:229-257) bit for bit: T shorter than a window, exactly
+    one window, a full last window, a short last window."""
+    ctx, model, ws, bs = env
+    say(f"windows edges T={T} win={win} ctx={cx}")
+    z = synth.latent(T, 300 + T)
+    ref = np.zeros(256 * T, np.float32)
+    a = emitted = 0
+    while emitted < T:
+        w = min(win, T - a)
+        last = a + w >= T
+        lo = 0 if a == 0 else cx
+        hi = w if last else w - cx
+        e0, e1 = max(a + lo, emitted), min(a + hi, T)
+        pcm = _decode(ctx, model, np.ascontiguousarray(z[:, a:a + w]))
+        if e1 > e0:
+            ref[e0 * 256:e1 * 256] = pcm[(e0 - a) * 256:(e1 - a) * 256]
+            emitted = e1
+        if last:
+            break
+        a = max(e1 - cx, 1)
+    dz, dw = dev_of(ctx, z), pkg.DevBuf.of(ctx, np.full(256 * T, np.nan, np.float32))
+    assert ctx.lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, win, cx, dw.ptr) == 0
+    wav = dw.download(ctx)
+    assert np.array_equal(wav, ref), f"max diff {np.nanmax(np.abs(wav - ref))}"
+    dz.free(); dw.free()
+
+
 def test_config5_longform_windows_vs_full(env):
     """T = 1500 through 96-frame windows with 16-frame context >= 60 dB from one full decode."""
     ctx, model, ws, bs = env
