@@ -216,9 +216,18 @@ __device__ __forceinline__ float epi_apply(float v, const ptk_epi &e, int b, int
 // Add / Div nodes in front of a conv, fused): IN is a PTK_IN_* code
 // LeakyReLU as max(v, a*v): identical to (v >= 0 ? v : a*v) for 0 <= a <= 1 (signed zeros
 // included), which the launcher enforces, in two instructions instead of three.
+// The division by 3 uses q = x * r, r = RN(1/3), corrected once with the exact residual
+// fma(-q, 3, x): checked exhaustively against IEEE x / 3 over every finite float, it differs only
+// for x = -0 (gives +0), which no conv output can tell apart.  Three instructions instead of the
+// ten of a general division.
 template <int IN>
 __device__ __forceinline__ float in_xform(float v, float v1, float v2, float a) {
-  if constexpr (IN == PTK_IN_AVG3_LEAKY) v = ((v + v1) + v2) / 3.0f;
+  if constexpr (IN == PTK_IN_AVG3_LEAKY) {
+    constexpr float r3 = 1.0f / 3.0f;
+    const float s = (v + v1) + v2;
+    const float q = s * r3;
+    v = __builtin_fmaf(__builtin_fmaf(-q, 3.0f, s), r3, q);
+  }
   if constexpr (IN != PTK_IN_PLAIN) v = fmaxf(v, a * v);
   return v;
 }
@@ -455,18 +464,29 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   // epilogue: the S partial sums of a block are added in wave order through LDS, then bias, the
   // epilogue chain and one store per output
   const long long qend = d.q0 + d.nq;
+  const int M = d.M, C4 = d.C4, ys = d.ys, ypad = d.ypad, nbias = d.nbias, nepi = d.nepi;
+  const long long Lout = d.Lout, ldy = d.ldy;
+  const float *bias = d.bias;
+  float *yb = d.y + (long long) b * d.bsy;
+  float *y2b = d.y2 != nullptr ? d.y2 + (long long) b * d.bsy : nullptr;
+  const float a2 = d.a2;
+  const bool phase_rows = C4 != M;   // convT: row m is phase m / C4 of channel m % C4
   auto emit = [&](int nb, int v, float sum) {
     const int m = mb * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
     const long long q = q0 + 32 * nb + l32;
-    if (m >= d.M || q >= qend) return;
-    const int co = m % d.C4, r = m / d.C4;
-    const long long col = q * d.ys + r - d.ypad;
-    if (col < 0 || col >= d.Lout) return;
-    float val = sum + ((d.bias != nullptr && co < d.nbias) ? d.bias[co] : 0.0f);
-    for (int e = 0; e < d.nepi; e++) val = epi_apply(val, d.epi[e], b, co, col);
-    const long long yi = (long long) b * d.bsy + (long long) co * d.ldy + col;
-    d.y[yi] = val;
-    if (d.y2 != nullptr) d.y2[yi] = val >= 0.0f ? val : d.a2 * val;
+    if (m >= M || q >= qend) return;
+    int co = m, r = 0;
+    if (phase_rows) {
+      r = m / C4;
+      co = m - r * C4;
+    }
+    const long long col = q * ys + r - ypad;
+    if (col < 0 || col >= Lout) return;
+    float val = sum + ((bias != nullptr && co < nbias) ? bias[co] : 0.0f);
+    for (int e = 0; e < nepi; e++) val = epi_apply(val, d.epi[e], b, co, col);
+    const long long yi = (long long) co * ldy + col;
+    yb[yi] = val;
+    if (y2b != nullptr) y2b[yi] = val >= 0.0f ? val : a2 * val;
   };
   if (S == 1) {
 #pragma unroll
