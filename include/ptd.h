@@ -31,14 +31,16 @@ int ptd_pool_load(pt_ctx *c, int n, const void *const *host, const size_t *bytes
 const void *ptd_pool_record(int i);
 
 /* ---- synthetic MB-iSTFT decoder (ref/v21_graph_trace.txt:3819-4065) ------------------------ *
- * 40 layers: 0 conv_pre, 1 ups.0, 2..19 MRF-256, 20 ups.1, 21..38 MRF-128, 39 conv_post; MRF
- * order branch (K 3,7,11) x dilation (1,3,5) x (c1, c2).  Weights in the packed layouts. */
-#define PTD_DEC_NLAYER 40
+ * 41 layers: 0 conv_pre, 1 ups.0, 2..19 MRF-256, 20 ups.1, 21..38 MRF-128, 39 conv_post, 40 the
+ * final PQMF synthesis conv /dec/Conv (4 -> 1, K 63, packed [1][63][4][4]; bias may be NULL);
+ * MRF order branch (K 3,7,11) x dilation (1,3,5) x (c1, c2).  Weights in the packed layouts. */
+#define PTD_DEC_NLAYER 41
 typedef struct ptd_model ptd_model;
 
-/* Uploads the 40 layers' weights and biases once into one device slab owned by the model and
- * shared by every context, lays every weight out for the MFMA kernels and builds the tail's
- * constant table.  Needs an initialised context (its stream does the upload).  NULL on failure. */
+/* Uploads the 41 layers' weights and biases once into one device slab owned by the model and
+ * shared by every context, lays every conv weight out for the MFMA kernels and builds the tail's
+ * table (closed-form Hann and irfft basis, layer 40's taps and bias).  Needs an initialised
+ * context (its stream does the upload).  NULL on failure. */
 ptd_model *ptd_model_create(pt_ctx *c, const float *const *w, const float *const *b);
 void ptd_model_destroy(ptd_model *m);
 
@@ -53,7 +55,7 @@ size_t ptd_decode_arena_bytes(int64_t T, int batch);
 int ptd_decode_stages(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, float *wav,
                       float *const *stages);
 
-/* Run decoder layer i alone: conv (x [batch][cin][T] -> y [batch][cout4][Tout]) or convT
+/* Run decoder layer i (0..39) alone: conv (x [batch][cin][T] -> y [batch][cout4][Tout]) or convT
  * (x [batch][cin][T] -> y [batch][cout4][Lout]).  in_leaky > 0 applies LeakyReLU(in_leaky) to
  * the input as it is read; epi_leaky > 0 applies it to the output.  Asynchronous. */
 int ptd_layer(pt_ctx *c, const ptd_model *m, int layer, const float *x, int64_t T, int batch,
@@ -115,8 +117,9 @@ float ptd_event_elapsed_ms(void *e0, void *e1); /* waits for e1; negative on err
 /* fp32 32x32x2 MFMA lane-layout probe (test hook): d[32][32] = a[32][2] @ b[2][32], host
  * buffers, synchronous on the context's stream. */
 int ptd_mfma_probe(pt_ctx *c, const float *a, const float *b, float *d);
-/* tail constant table as the device uses it (host copy, PTD_TAIL_NCONST floats) */
-#define PTD_TAIL_NCONST (16 + 144 + 144 + 252)
+/* closed-form part of the tail table as the device uses it (host copy, PTD_TAIL_NCONST floats):
+ * periodic Hann(16), irfft basis cos rows (9 x 16), -sin rows (9 x 16) */
+#define PTD_TAIL_NCONST (16 + 144 + 144)
 void ptd_tail_constants(float *out);
 /* offsets of the pt_ctx fields the device layer touches (for the ABI test) */
 int ptd_ctx_layout(long *out, int n);

@@ -187,17 +187,7 @@ static float *pack_convT_c(const float *W, int cin, int cout, int K, int s) {
  * PQMF: /dec/Constant_134 is a model constant (only 8 of 252 values are visible in the trace), so
  * the synthetic decoder fixes its own: the Kaiser-windowed sinc prototype with 62 taps, cutoff
  * 0.142, beta 9, cosine-modulated for 4 bands with phase -(-1)^k pi/4, gain 2. */
-static double bessel_i0(double x) {
-  double sum = 1.0, term = 1.0, q = x * x / 4.0;
-  for (int k = 1; k < 200; k++) {
-    term *= q / ((double) k * (double) k);
-    sum += term;
-    if (term < sum * 1e-17) break;
-  }
-  return sum;
-}
-
-void orc_dec_constants(float *hann16, float *basis_c, float *basis_s, float *pqmf_syn) {
+void orc_dec_constants(float *hann16, float *basis_c, float *basis_s) {
   const double pi = 3.14159265358979323846;
   if (hann16)
     for (int n = 0; n < 16; n++) hann16[n] = (float) (0.5 - 0.5 * cos(2.0 * pi * n / 16.0));
@@ -206,24 +196,6 @@ void orc_dec_constants(float *hann16, float *basis_c, float *basis_s, float *pqm
     for (int n = 0; n < 16; n++) {
       if (basis_c) basis_c[k * 16 + n] = (float) (w * cos(2.0 * pi * k * n / 16.0) / 16.0);
       if (basis_s) basis_s[k * 16 + n] = (float) (-w * sin(2.0 * pi * k * n / 16.0) / 16.0);
-    }
-  }
-  if (pqmf_syn) {
-    const int taps = 62;
-    const double cutoff = 0.142, beta = 9.0, wc = pi * cutoff;
-    double proto[63];
-    for (int n = 0; n <= taps; n++) {
-      const double m = n - 0.5 * taps;
-      double h = (n == taps / 2) ? cutoff : sin(wc * m) / (pi * m);
-      const double r = 2.0 * n / taps - 1.0;
-      h *= bessel_i0(beta * sqrt(1.0 - r * r)) / bessel_i0(beta);
-      proto[n] = h;
-    }
-    for (int k = 0; k < 4; k++) {
-      const double sg = (k % 2 == 0) ? 1.0 : -1.0;
-      for (int n = 0; n <= taps; n++)
-        pqmf_syn[k * 63 + n] = (float) (2.0 * proto[n] *
-                                        cos((2 * k + 1) * (pi / 8.0) * (n - 0.5 * taps) - sg * pi / 4.0));
     }
   }
 }
@@ -244,6 +216,8 @@ int orc_dec_layer(int i, int *cin, int *cout, int *K, int *sd, int *pad, int *is
     *K = 16; *sd = 4; *pad = 6; *is_convT = 1; return 0;
   }
   if (i == 39) { *cin = 128; *cout = 72; *K = 7; *sd = 1; *pad = 3; return 0; }
+  /* /dec/Conv: its input is padded by the /dec/Pad node (31|31) before it, so the conv has pad 0 */
+  if (i == 40) { *cin = 4; *cout = 1; *K = 63; *sd = 1; *pad = 0; return 0; }
   const int base = i < 20 ? 2 : 21, C = i < 20 ? 256 : 128;
   const int o = i - base, b = o / 6, j = (o % 6) / 2, c = o % 2;
   *cin = C; *cout = C; *K = kMrfK[b];
@@ -336,9 +310,9 @@ done:
  * double rounded to fp32 (pt_v21_host.c:625-647), scalar Mul/Div/Add in fp32 (:450-494), the
  * bkt,kn->bnt einsum accumulated in double over k ascending (:1963-1995), Clip as a compare,
  * the three ConvTransposes and the final Conv through the conv/convT path with packed kernels. */
-int orc_tail(const float *p, int64_t L, float *wav) {
-  float hann[16], bc[144], bs[144], syn[4 * 63];
-  orc_dec_constants(hann, bc, bs, syn);
+int orc_tail(const float *p, int64_t L, const float *wfir, const float *bfir, float *wav) {
+  float hann[16], bc[144], bs[144];
+  orc_dec_constants(hann, bc, bs);
   const int64_t Lola = (L - 1) * 4 + 16, Ly = Lola - 16, Lu = Ly * 4;
   float *mag = malloc(36 * L * sizeof(float)), *ph = malloc(36 * L * sizeof(float));
   float *re = malloc(36 * L * sizeof(float)), *im = malloc(36 * L * sizeof(float));
@@ -347,7 +321,7 @@ int orc_tail(const float *p, int64_t L, float *wav) {
   float *ola = malloc(4 * Lola * sizeof(float)), *ones = malloc(4 * L * sizeof(float));
   float *wsum = malloc(4 * Lola * sizeof(float)), *yv = malloc(4 * Ly * sizeof(float));
   float *u = malloc(4 * Lu * sizeof(float)), *up = malloc(4 * (Lu + 62) * sizeof(float));
-  float *W = NULL, *wola = NULL, *wwin = NULL, *wup = NULL, *wfir = NULL;
+  float *W = NULL, *wola = NULL, *wwin = NULL, *wup = NULL;
   int rc = -1;
   if (!mag || !ph || !re || !im || !fr || !fi || !acc || !ola || !ones || !wsum || !yv || !u || !up)
     goto done;
@@ -410,16 +384,15 @@ int orc_tail(const float *p, int64_t L, float *wav) {
   float wu[64] = {0};
   for (int c = 0; c < 4; c++) wu[(c * 4 + c) * 4 + 0] = 4.0f;
   wup = pack_convT_c(wu, 4, 4, 4, 4);
-  wfir = pack_conv_c(syn, 1, 4, 63);
   if (!wup || !wfir) goto done;
   if (convT_node(yv, Ly, 4, 4, 4, 4, 0, wup, NULL, u, 1)) goto done;
   /* /dec/Pad (constant 31|31) feeds a pad-0 conv: the conv node's scratch is that padded row */
   orc_pad_rows(u, 1, 4, Lu, 31, up);
-  if (conv_node(up, Lu + 62, 4, 1, 63, 0, 1, wfir, NULL, 0, 0.0f, wav, 1)) goto done;
+  if (conv_node(up, Lu + 62, 4, 1, 63, 0, 1, wfir, bfir, 0, 0.0f, wav, 1)) goto done;
   rc = 0;
 done:
   free(mag); free(ph); free(re); free(im); free(fr); free(fi); free(acc); free(ola); free(ones);
-  free(wsum); free(yv); free(u); free(up); free(W); free(wola); free(wwin); free(wup); free(wfir);
+  free(wsum); free(yv); free(u); free(up); free(W); free(wola); free(wwin); free(wup);
   return rc;
 }
 
@@ -459,7 +432,7 @@ int orc_decoder(const orc_dec_weights *W, const float *z, int64_t T, float *wav,
     for (int s = 0; s < 6; s++)
       if (stages[s]) memcpy(stages[s], src[s], orc_dec_stage_len(s, T) * sizeof(float));
   }
-  if (orc_tail(pp, L, wav)) goto done;
+  if (orc_tail(pp, L, W->w[40], W->b[40], wav)) goto done;
   rc = 0;
 done:
   free(h); free(x0); free(m0); free(x1); free(m1); free(rp); free(pp);

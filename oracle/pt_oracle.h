@@ -54,9 +54,11 @@ void orc_leaky(const float *a, float *o, int64_t n, float alpha);
 /* ---------------------------------------------------------------- synthetic MB-iSTFT decoder
  * Topology: ref/v21_graph_trace.txt:3819-4065 (conv_pre .. /dec/Conv).  Layer order of the
  * weight arrays (ORC_DEC_NLAYER entries): 0 conv_pre, 1 ups.0, 2..19 MRF-256, 20 ups.1,
- * 21..38 MRF-128, 39 conv_post.  Inside an MRF: branch b (K = 3, 7, 11), dilation j
- * (1, 3, 5), conv c (c1, c2) at index 2 + 18*stage_offset + b*6 + j*2 + c. */
-#define ORC_DEC_NLAYER 40
+ * 21..38 MRF-128, 39 conv_post, 40 the final PQMF synthesis conv /dec/Conv (4 -> 1, K 63, its
+ * weight the model constant /dec/Constant_134; bias may be NULL).  Inside an MRF: branch b
+ * (K = 3, 7, 11), dilation j (1, 3, 5), conv c (c1, c2) at index 2 + 18*stage_offset + b*6 +
+ * j*2 + c. */
+#define ORC_DEC_NLAYER 41
 #define ORC_DEC_ZCH 192
 #define ORC_DEC_STAGES 6
 
@@ -68,9 +70,9 @@ typedef struct {
 /* geometry of layer i: cin, cout, K, stride(convT)/dilation(conv), pad, is_convT */
 int orc_dec_layer(int i, int *cin, int *cout, int *K, int *sd, int *pad, int *is_convT);
 
-/* Fixed constants of the synthetic decoder tail: periodic Hann(16), irfft basis (9 x 16, cos and
- * -sin rows, one-sided weights, /16), PQMF synthesis filter (4 x 63) and its prototype. */
-void orc_dec_constants(float *hann16, float *basis_c, float *basis_s, float *pqmf_syn);
+/* Fixed constants of the decoder tail that the op definitions determine: periodic Hann(16) and
+ * the irfft basis (9 x 16, cos and -sin rows, one-sided weights, /16). */
+void orc_dec_constants(float *hann16, float *basis_c, float *basis_s);
 
 /* Run the decoder for z [192][T]; wav receives 256*T samples.  stages (optional, may be NULL)
  * receives copies of: 0 conv_pre+leaky [512][T], 1 ups.0 [256][4T], 2 MRF-256 output after
@@ -83,8 +85,9 @@ int64_t orc_dec_stage_len(int stage, int64_t T);   /* floats in stage buffer */
 int orc_mrf(const float *const *wt, const float *const *bt, int C, int64_t T, const float *x,
             float alpha, float *out);
 
-/* Tail alone: conv_post output p [72][L] -> wav [4*4*(L-1)] (trace :3936-4065). */
-int orc_tail(const float *p, int64_t L, float *wav);
+/* Tail alone: conv_post output p [72][L] -> wav [4*4*(L-1)] (trace :3936-4065); wfir / bfir:
+ * the packed weight ([1][63][4][4]) and bias (NULL: none) of the final PQMF conv. */
+int orc_tail(const float *p, int64_t L, const float *wfir, const float *bfir, float *wav);
 
 #ifdef __cplusplus
 }

@@ -83,7 +83,7 @@ CTX_FIELDS = ["use_cuda", "n_conv", "n_convT", "n_matmul", "g_alloc_ms", "g_call
               "dev_bytes_weights", "dev_bytes_res", "devres_oom", "arena_alloc_bytes", "g_weights",
               "g_arena", "g_stream", "g_arena_bytes", "g_arena_used", "conv_pad_in", "conv_in_dev",
               "conv_keep", "conv_keep_res", "dev_live", "conv_out_dev", "chain_mark", "devres"]
-TAIL_NCONST = 16 + 144 + 144 + 252
+TAIL_NCONST = 16 + 144 + 144   # closed-form part of the tail table (Hann, irfft basis)
 
 
 class Request(C.Structure):
@@ -223,8 +223,9 @@ class Model:
         self.lib = load()
         self._ws = [np.ascontiguousarray(w, np.float32) for w in ws]
         self._bs = [np.ascontiguousarray(b, np.float32) for b in bs]
-        wa = (F * 40)(*[fptr(w) for w in self._ws])
-        ba = (F * 40)(*[fptr(b) for b in self._bs])
+        assert len(self._ws) == synth.N_LAYER and len(self._bs) == synth.N_LAYER
+        wa = (F * synth.N_LAYER)(*[fptr(w) for w in self._ws])
+        ba = (F * synth.N_LAYER)(*[fptr(b) for b in self._bs])
         self.ptr = self.lib.ptd_model_create(ctx.ptr, wa, ba)
         if not self.ptr:
             raise RuntimeError("ptd_model_create failed")

@@ -40,6 +40,8 @@ static layer_geo dec_geo(int i) {
     g.cin = i == 1 ? 512 : 256; g.cout = i == 1 ? 256 : 128; g.K = 16; g.sd = 4; g.pad = 6; g.convT = 1;
   } else if (i == 39) {
     g.cin = 128; g.cout = 72; g.K = 7; g.pad = 3;
+  } else if (i == 40) {   /* /dec/Conv after /dec/Pad 31|31: 4 -> 1, K 63 */
+    g.cin = 4; g.cout = 1; g.K = 63; g.pad = 0;
   } else {
     const int base = i < 20 ? 2 : 21, C = i < 20 ? 256 : 128, o = i - base;
     const int br = o / 6, j = (o % 6) / 2, c = o % 2;
@@ -60,13 +62,12 @@ struct ptd_model {
 
 static size_t al256(size_t b) { return (b + 255) & ~(size_t) 255; }
 
-/* Constants of the tail (the same closed forms the reference graph folds into constants):
+/* Closed-form constants of the tail (the reference graph folds the same values into constants):
  * periodic Hann(16); irfft basis rows w_k cos(2 pi k n / 16) / 16 and -w_k sin(...) / 16 with
- * one-sided weights w = [1, 2, ..., 2, 1]; PQMF synthesis filters from the Kaiser-windowed sinc
- * prototype (62 taps, cutoff 0.142, beta 9), cosine-modulated for 4 bands, gain 2. */
+ * one-sided weights w = [1, 2, ..., 2, 1]. */
 void ptd_tail_constants(float *out) {
   const double pi = 3.14159265358979323846;
-  float *hann = out, *bc = out + 16, *bs = out + 160, *h = out + 304;
+  float *hann = out, *bc = out + 16, *bs = out + 160;
   for (int n = 0; n < 16; n++) hann[n] = (float) (0.5 - 0.5 * cos(2.0 * pi * n / 16.0));
   for (int k = 0; k < 9; k++) {
     const double w = (k == 0 || k == 8) ? 1.0 : 2.0;
@@ -75,31 +76,14 @@ void ptd_tail_constants(float *out) {
       bs[k * 16 + n] = (float) (-w * sin(2.0 * pi * k * n / 16.0) / 16.0);
     }
   }
-  /* modified Bessel I0 by its power series (converges fast for the beta used here) */
-  double i0b = 1.0, term = 1.0;
-  for (int k = 1; k < 200; k++) {
-    term *= (81.0 / 4.0) / ((double) k * k);
-    i0b += term;
-    if (term < 1e-17 * i0b) break;
-  }
-  double proto[63];
-  for (int n = 0; n <= 62; n++) {
-    const double m = n - 31.0;
-    double v = n == 31 ? 0.142 : sin(pi * 0.142 * m) / (pi * m);
-    const double r = 2.0 * n / 62.0 - 1.0, x = 9.0 * sqrt(1.0 - r * r);
-    double i0 = 1.0, t = 1.0;
-    for (int k = 1; k < 200; k++) {
-      t *= (x * x / 4.0) / ((double) k * k);
-      i0 += t;
-      if (t < 1e-17 * i0) break;
-    }
-    proto[n] = v * i0 / i0b;
-  }
-  for (int k = 0; k < 4; k++) {
-    const double sg = (k & 1) ? -1.0 : 1.0;
-    for (int n = 0; n <= 62; n++)
-      h[k * 63 + n] = (float) (2.0 * proto[n] * cos((2 * k + 1) * (pi / 8.0) * (n - 31.0) - sg * pi / 4.0));
-  }
+}
+
+/* the final conv's taps h[band*63 + m] = W[0][band][m] out of its packed weight [1][63][4][4]
+ * (row 0 of the first row block), then its bias (0 without one) */
+static void tail_fir(float *dst, const float *wp, const float *bias) {
+  for (int band = 0; band < 4; band++)
+    for (int m = 0; m < 63; m++) dst[band * 63 + m] = wp[((size_t) m * 4 + band) * 4 + 0];
+  dst[252] = bias ? bias[0] : 0.0f;
 }
 
 ptd_model *ptd_model_create(pt_ctx *c, const float *const *w, const float *const *b) {
@@ -108,7 +92,12 @@ ptd_model *ptd_model_create(pt_ctx *c, const float *const *w, const float *const
   if (!m) return NULL;
   size_t total = 0, packed_max = 0;
   size_t off_w[PTD_DEC_NLAYER], off_b[PTD_DEC_NLAYER], wbytes[PTD_DEC_NLAYER];
-  for (int i = 0; i < PTD_DEC_NLAYER; i++) {
+  if (!w[PTD_DEC_NLAYER - 1]) {
+    PT_LOG("ptd_model_create: layer %d (the PQMF synthesis conv) has no weight", PTD_DEC_NLAYER - 1);
+    free(m);
+    return NULL;
+  }
+  for (int i = 0; i < PTD_DEC_NLAYER - 1; i++) {
     layer_geo g = dec_geo(i);
     m->g[i] = g;
     const int c4 = (g.cout + 3) / 4 * 4;
@@ -120,14 +109,16 @@ ptd_model *ptd_model_create(pt_ctx *c, const float *const *w, const float *const
     off_b[i] = total;
     total += al256((size_t) g.cout * sizeof(float));
   }
+  m->g[PTD_DEC_NLAYER - 1] = dec_geo(PTD_DEC_NLAYER - 1);
   const size_t off_c = total;
-  total += al256(PTD_TAIL_NCONST * sizeof(float));
-  float consts[PTD_TAIL_NCONST];
+  total += al256(PTK_TAIL_NCONST * sizeof(float));
+  float consts[PTK_TAIL_NCONST];
   ptd_tail_constants(consts);
+  tail_fir(consts + PTD_TAIL_NCONST, w[PTD_DEC_NLAYER - 1], b[PTD_DEC_NLAYER - 1]);
   void *tmp = NULL;
   if (ptk_malloc(&m->slab, total) || ptk_malloc(&tmp, packed_max)) goto fail;
   char *base = (char *) m->slab;
-  for (int i = 0; i < PTD_DEC_NLAYER; i++) {
+  for (int i = 0; i < PTD_DEC_NLAYER - 1; i++) {
     const layer_geo g = m->g[i];
     const int c4 = (g.cout + 3) / 4 * 4;
     const int M = g.convT ? g.sd * c4 : c4, K = g.convT ? (g.K + g.sd - 1) / g.sd : g.K;
@@ -349,7 +340,7 @@ int ptd_decode_stages(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, 
 
 int ptd_layer(pt_ctx *c, const ptd_model *m, int layer, const float *x, int64_t T, int batch,
               float *y, float in_leaky, float epi_leaky) {
-  if (!c || !c->use_cuda || !m || layer < 0 || layer >= PTD_DEC_NLAYER || T < 1 || batch < 1) return -1;
+  if (!c || !c->use_cuda || !m || layer < 0 || layer >= PTD_DEC_NLAYER - 1 || T < 1 || batch < 1) return -1;
   const layer_geo g = m->g[layer];
   ptk_conv_desc d;
   if (g.convT) {

@@ -835,7 +835,7 @@ __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, 
   __shared__ float s_y[4][TAIL_NY];
   const int tid = threadIdx.x;
   for (int i = tid; i < PTK_TAIL_NCONST; i += 256) s_c[i] = cst[i];
-  const float *hann = s_c, *bc = s_c + 16, *bs = s_c + 160, *h = s_c + 304;
+  const float *hann = s_c, *bc = s_c + 16, *bs = s_c + 160, *h = s_c + 304, *hb = s_c + 556;
   const long long Ly = 4 * (L - 1);
   const long long nout = 4 * Ly;
   const long long o0 = (long long) blockIdx.x * TAIL_OUT;
@@ -910,7 +910,7 @@ __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, 
       acc += h[b * 63 + m] * (4.0f * s_y[b][(int) (i - i_lo)]);
     }
   }
-  if (o >= e_lo && o < e_hi) wav[o] = acc;
+  if (o >= e_lo && o < e_hi) wav[o] = acc + hb[0];
 }
 
 extern "C" int ptk_tail_batched(const float *p, int64_t ldp, int64_t bsp, int64_t L, float *wav,

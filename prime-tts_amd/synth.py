@@ -17,10 +17,13 @@ from __future__ import annotations
 
 import numpy as np
 
+import pathlib
+
 MRF_K = (3, 7, 11)
 MRF_D = (1, 3, 5)
-N_LAYER = 40
+N_LAYER = 41          # 40 conv layers + the final PQMF synthesis conv (/dec/Conv)
 Z_CH = 192
+PQMF_FILE = pathlib.Path(__file__).resolve().parent / "data" / "v21_pqmf_synthesis.npy"
 
 
 def r4(n: int) -> int:
@@ -78,6 +81,8 @@ def dec_layer(i: int) -> dict:
                     pad=6, convT=True)
     if i == 39:
         return dict(cin=128, cout=72, K=7, s=1, d=1, pad=3, convT=False)
+    if i == 40:   # /dec/Conv after /dec/Pad 31|31: 4 subbands -> 1, K 63, fixed weights
+        return dict(cin=4, cout=1, K=63, s=1, d=1, pad=0, convT=False)
     base, C = (2, 256) if i < 20 else (21, 128)
     o = i - base
     b, j, c = o // 6, (o % 6) // 2, o % 2
@@ -98,13 +103,29 @@ def convT_weights(rng: np.random.Generator, cin: int, cout: int, K: int, s: int)
     return W.astype(np.float32), b.astype(np.float32)
 
 
+def pqmf_synthesis() -> np.ndarray:
+    """The model's PQMF synthesis filter, /dec/Constant_134 (1, 4, 63): the weight of the
+    decoder's last conv (data/v21_pqmf_synthesis.npy, decoded from the reference's
+    spec/v21_layers.json by data/extract_constants.py)."""
+    h = np.load(PQMF_FILE, allow_pickle=False)
+    assert h.shape == (1, 4, 63) and h.dtype == np.float32
+    return h
+
+
 def decoder_weights(seed: int = 1234, raw: bool = False):
-    """Packed weights + biases of the 40 decoder layers (synthetic, random-init).  With raw=True
-    the ONNX-layout weights are returned too (conv [Cout][Cin][K], convT [Cin][Cout][K])."""
+    """Packed weights + biases of the 41 decoder layers: the 40 convs synthetic and random-init,
+    layer 40 the model's own PQMF synthesis conv (no bias).  With raw=True the ONNX-layout
+    weights are returned too (conv [Cout][Cin][K], convT [Cin][Cout][K])."""
     rng = np.random.default_rng(seed)
     ws, bs, raws = [], [], []
     for i in range(N_LAYER):
         g = dec_layer(i)
+        if i == 40:
+            W = pqmf_synthesis()
+            ws.append(pack_conv(W))
+            bs.append(np.zeros(1, np.float32))
+            raws.append(W)
+            continue
         if g["convT"]:
             W, b = convT_weights(rng, g["cin"], g["cout"], g["K"], g["s"])
             ws.append(pack_convtranspose(W, g["s"]))

@@ -1,7 +1,7 @@
 """Float64 NumPy restatement of the synthetic decoder from the ONNX operator definitions, written
 independently of the packed layouts: conv / convTranspose by explicit index scatter (the form of
 tools/export_v21.py:967-1000 conv1d_brute / conv_transpose1d_brute), the iSTFT through
-numpy.fft.irfft, the window through its closed form and the PQMF prototype through numpy.kaiser.
+numpy.fft.irfft, the window through its closed form and the PQMF synthesis as a plain conv.
 It pins the C oracle from the mathematics side: a dropped term, a wrong sign or index, or a
 transposed operand in the oracle shows up as a large error against this."""
 from __future__ import annotations
@@ -53,19 +53,6 @@ def hann16():
     return 0.5 - 0.5 * np.cos(2 * np.pi * n / 16)
 
 
-def pqmf_synthesis(taps=62, cutoff=0.142, beta=9.0, bands=4):
-    n = np.arange(taps + 1)
-    m = n - 0.5 * taps
-    with np.errstate(invalid="ignore", divide="ignore"):
-        h = np.sin(np.pi * cutoff * m) / (np.pi * m)
-    h[taps // 2] = cutoff
-    h = h * np.kaiser(taps + 1, beta)
-    syn = np.zeros((bands, taps + 1))
-    for k in range(bands):
-        syn[k] = 2 * h * np.cos((2 * k + 1) * (np.pi / (2 * bands)) * m - (-1) ** k * np.pi / 4)
-    return syn
-
-
 def mrf(raw, bias, x, alpha):
     l0 = leaky(x, 0.1)
     outs = []
@@ -80,8 +67,9 @@ def mrf(raw, bias, x, alpha):
     return leaky((outs[0] + outs[1] + outs[2]) / 3.0, alpha)
 
 
-def tail(p):
-    """conv_post output p [72][L] -> waveform [16(L-1)] via irfft, Hann OLA and PQMF synthesis."""
+def tail(p, syn, syn_bias=None):
+    """conv_post output p [72][L] -> waveform [16(L-1)] via irfft, Hann OLA and PQMF synthesis;
+    syn [4][63]: the weight of the final conv (/dec/Conv), syn_bias its bias (or None)."""
     p = np.asarray(p, np.float64)
     L = p.shape[-1]
     win = hann16()
@@ -98,13 +86,15 @@ def tail(p):
             ola[4 * t:4 * t + 16] += frames[:, t]
             wsum[4 * t:4 * t + 16] += win ** 2
         ys[band] = (ola / np.maximum(wsum, 1e-9))[8:-8]
-    syn = pqmf_synthesis()
+    syn = np.asarray(syn, np.float64).reshape(4, 63)
     u = np.zeros((4, 4 * Ly))
     u[:, ::4] = 4.0 * ys
     up = np.pad(u, ((0, 0), (31, 31)))
     wav = np.zeros(4 * Ly)
     for band in range(4):
         wav += np.convolve(up[band], syn[band][::-1], mode="valid")
+    if syn_bias is not None:
+        wav += float(np.asarray(syn_bias).ravel()[0])
     return wav
 
 
@@ -116,7 +106,7 @@ def decoder(raw, bias, z):
     m1 = mrf(raw[21:39], bias[21:39], x1, 0.01)
     rp = np.concatenate([m1[:, 1:2], m1], axis=1)
     p = conv1d(rp, raw[39], bias[39], 1, 3, 1)
-    return tail(p), dict(h=h, x0=x0, m0=m0, x1=x1, m1=m1, p=p)
+    return tail(p, raw[40], bias[40]), dict(h=h, x0=x0, m0=m0, x1=x1, m1=m1, p=p)
 
 
 def sndr(est, ref):

@@ -40,8 +40,8 @@ def oracle():
         lib.orc_epi.restype = C.c_float
         lib.orc_decoder.argtypes = [C.c_void_p, F, I64, F, C.POINTER(F)]
         lib.orc_mrf.argtypes = [C.POINTER(F), C.POINTER(F), C.c_int, I64, F, C.c_float, F]
-        lib.orc_tail.argtypes = [F, I64, F]
-        lib.orc_dec_constants.argtypes = [F, F, F, F]
+        lib.orc_tail.argtypes = [F, I64, F, F, F]
+        lib.orc_dec_constants.argtypes = [F, F, F]
         lib.orc_dec_stage_len.argtypes = [C.c_int, I64]
         lib.orc_dec_stage_len.restype = I64
         lib.orc_set_conv_impl.argtypes = [C.c_void_p, C.c_void_p]
@@ -107,13 +107,17 @@ def convT(x, wp, bias, cout, K, s, pad, lib=None):
     return y
 
 
+N_DEC = 41   # 40 conv layers + the final PQMF synthesis conv (oracle/pt_oracle.h ORC_DEC_NLAYER)
+
+
 class DecWeights(C.Structure):
-    _fields_ = [("w", F * 40), ("b", F * 40)]
+    _fields_ = [("w", F * N_DEC), ("b", F * N_DEC)]
 
 
 def dec_weights_struct(ws, bs):
+    assert len(ws) == N_DEC and len(bs) == N_DEC
     st = DecWeights()
-    for i in range(40):
+    for i in range(N_DEC):
         st.w[i] = fptr(ws[i])
         st.b[i] = fptr(bs[i])
     return st
@@ -153,11 +157,15 @@ def mrf(wts, bts, x, alpha):
     return out
 
 
-def tail(p):
+def tail(p, wfir, bfir=None):
+    """wfir / bfir: packed weight and bias of the final PQMF conv (decoder layer 40)."""
     lib = oracle()
     L = p.shape[-1]
     wav = np.zeros(16 * (L - 1), np.float32)
-    assert lib.orc_tail(fptr(np.ascontiguousarray(p, np.float32)), L, fptr(wav)) == 0
+    assert lib.orc_tail(fptr(np.ascontiguousarray(p, np.float32)), L,
+                        fptr(np.ascontiguousarray(wfir, np.float32)),
+                        fptr(None if bfir is None else np.ascontiguousarray(bfir, np.float32)),
+                        fptr(wav)) == 0
     return wav
 
 
@@ -165,6 +173,5 @@ def constants():
     hann = np.zeros(16, np.float32)
     bc = np.zeros(144, np.float32)
     bs = np.zeros(144, np.float32)
-    syn = np.zeros(4 * 63, np.float32)
-    oracle().orc_dec_constants(fptr(hann), fptr(bc), fptr(bs), fptr(syn))
-    return hann, bc.reshape(9, 16), bs.reshape(9, 16), syn.reshape(4, 63)
+    oracle().orc_dec_constants(fptr(hann), fptr(bc), fptr(bs))
+    return hann, bc.reshape(9, 16), bs.reshape(9, 16)

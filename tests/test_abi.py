@@ -60,11 +60,11 @@ def test_tail_constants_match_oracle():
     import ctypes as C
     out = np.zeros(pkg.TAIL_NCONST, np.float32)
     lib.ptd_tail_constants(out.ctypes.data_as(C.POINTER(C.c_float)))
-    hann, bc, bs, syn = ol.constants()
+    hann, bc, bs = ol.constants()
+    assert out.size == 304
     assert np.array_equal(out[:16], hann)
     assert np.array_equal(out[16:160], bc.ravel())
     assert np.array_equal(out[160:304], bs.ravel())
-    assert np.allclose(out[304:], syn.ravel(), rtol=0, atol=2e-8)
 
 
 def test_host_only_calls_fail_loudly_without_device():

@@ -146,6 +146,24 @@ def test_config4_decoder_T226_vs_oracle(env):
     assert np_ref.sndr(wav, ref) >= 60.0
 
 
+def test_decoder_final_conv_is_an_input():
+    """The final PQMF synthesis conv (layer 40) comes from the caller's weights: a random filter
+    with a bias gives the oracle's waveform, not the model constant's."""
+    say("decoder with a random final conv and bias, T=20")
+    ctx = pkg.Ctx(arena_mb=256)
+    ws, bs = synth.decoder_weights(99)
+    rng = np.random.default_rng(40)
+    W = (rng.standard_normal((1, 4, 63)) * 0.05).astype(np.float32)
+    ws[40] = synth.pack_conv(W)
+    bs[40] = np.array([0.25], np.float32)
+    model = pkg.Model(ctx, ws, bs)
+    z = synth.latent(20, 40)
+    ref = ol.decoder(ws, bs, z)
+    wav = _decode(ctx, model, z)
+    model.close(); ctx.close()
+    assert np_ref.sndr(wav, ref) >= 60.0
+
+
 def test_batched_decode_matches_single(env):
     """batch > 1 (used by the windowed path) equals per-item decodes bit for bit."""
     ctx, model, ws, bs = env

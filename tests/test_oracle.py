@@ -4,6 +4,8 @@ definitions, torch's CPU conv1d / conv_transpose1d, closed forms, invariants, an
 mutation trials of the reference's docs (docs/v21_layers.md:103-106), each of which must fail."""
 from __future__ import annotations
 
+import pathlib
+
 import numpy as np
 import pytest
 import torch
@@ -202,7 +204,7 @@ def test_layout_mutations_fail():
 
 # ---------------------------------------------------------------- decoder and constants
 def test_constants_closed_forms():
-    hann, bc, bs, syn = ol.constants()
+    hann, bc, bs = ol.constants()
     assert np.allclose(hann, np_ref.hann16(), atol=1e-7)
     # the trace's own preview values of /dec/Constant_109 (ref/v21_graph_trace.txt:4009)
     assert np.allclose(hann[:8], [0.0, 0.03806025, 0.14644662, 0.3086583, 0.5, 0.69134176,
@@ -211,7 +213,30 @@ def test_constants_closed_forms():
     spec = rng.standard_normal((9, 7)) + 1j * rng.standard_normal((9, 7))
     frames = bc.T.astype(np.float64) @ spec.real + bs.T.astype(np.float64) @ spec.imag
     assert np.allclose(frames, np.fft.irfft(spec, n=16, axis=0), atol=1e-6)
-    assert np.allclose(syn, np_ref.pqmf_synthesis(), atol=1e-7)
+
+
+def test_pqmf_filter_is_the_models():
+    """The decoder's last conv weight is the model constant /dec/Constant_134 (1, 4, 63).  The
+    packaged copy must equal the trace's own preview of it (ref/v21_graph_trace.txt:4064) and, where
+    the reference tree exists, the full raw bytes in spec/v21_layers.json."""
+    h = synth.pqmf_synthesis()
+    assert h.shape == (1, 4, 63)
+    assert np.array_equal(h.ravel()[:8], np.array(
+        [1.6410408e-05, 5.2573592e-05, 8.4096690e-05, 6.8166526e-05, 1.0740955e-05,
+         3.3666347e-05, 3.3252931e-04, 9.7845600e-04], np.float32))
+    spec_file = pathlib.Path("/root/reference/spec/v21_layers.json")
+    if spec_file.exists():
+        import importlib.util
+        ex = ROOT / "prime-tts_amd" / "data" / "extract_constants.py"
+        sp = importlib.util.spec_from_file_location("extract_constants", ex)
+        mod = importlib.util.module_from_spec(sp)
+        sp.loader.exec_module(mod)
+        import json
+        ref = mod.constant(json.loads(spec_file.read_text()), "/dec/Constant_134")
+        assert np.array_equal(ref, h)
+    # a cosine-modulated synthesis bank: band 0 carries the DC gain, the others sum to ~0
+    sums = h[0].astype(np.float64).sum(axis=1)
+    assert abs(sums[0] - 1.314) < 1e-3 and np.all(np.abs(sums[1:]) < 1e-4)
 
 
 @pytest.mark.parametrize("T", [4, 9])
