@@ -30,6 +30,36 @@ int ptd_pool_load(pt_ctx *c, int n, const void *const *host, const size_t *bytes
 /* device pointer of pool record i, or NULL */
 const void *ptd_pool_record(int i);
 
+/* ---- .ptk weight container (tools/export_v21.py:5-23, :232-274; C reader
+ * runtime/v21/src/pt_v21_host.c:1086-1220, fp16 rule :653-673) ------------------------------ *
+ * Header <IIIiq (magic 'PTK1', version, n_tensor, reserved, data_bytes), n records <64si4x6qqq
+ * (name, ndim, dim[6], nelem, offset), 64-byte aligned payloads; bytes per item from the fp32
+ * record "dtype.table" (4 fp32, 2 fp16), which must be present, as for the reference's reader.
+ * The file is read whole into host memory and every range is checked: a truncated or corrupt
+ * container is refused (NULL / -1 and a "pt_v21 hip: ptk:" line on stderr). */
+typedef struct ptd_ptk ptd_ptk;
+ptd_ptk *ptd_ptk_open(const char *path);      /* replaces the record pass of pt_v21_open */
+void ptd_ptk_close(ptd_ptk *f);
+int ptd_ptk_count(const ptd_ptk *f);          /* number of records */
+int ptd_ptk_find(const ptd_ptk *f, const char *name);   /* first record of that name, or -1 */
+/* record i: name (65 bytes, NUL-terminated), ndim, dims[6], nelem, bytes per item; 0 / -1 */
+int ptd_ptk_info(const ptd_ptk *f, int i, char *name, int *ndim, int64_t *dims, int64_t *nelem,
+                 int *itemsize);
+const void *ptd_ptk_payload(const ptd_ptk *f, int i);   /* raw payload bytes (host), or NULL */
+/* record i as fp32 on the host (n must equal its nelem): fp16 expands exactly, subnormals kept,
+ * inf / NaN keep sign and payload (the reference's half2float_bits, pt_v21_host.c:653-673) */
+int ptd_ptk_read_f32(const ptd_ptk *f, int i, float *out, int64_t n);
+/* 0 when the container holds a v2.1 decoder this library runs: the 41 layers' dec.*.wp[#h] /
+ * dec.*.b records at their packed sizes and the three fixed tail convTs (dec.ConvTranspose,
+ * _1, _2) in the forms the fused tail implements; else -1 naming the first problem */
+int ptd_ptk_check_decoder(const ptd_ptk *f);
+/* Load the process weight pool from the container: pool record k = the record named ctab[k]
+ * (the graph's constant table, gen/pt_graph.c pt_graph_ctab; NULL or absent names leave record
+ * k empty).  fp16 payloads go up as fp16 and expand on the device.  Same pool and same rules as
+ * ptd_pool_load; this is the container route of the reference's weights_upload
+ * (pt_v21_cuda.cu:90-235), without a host fp32 copy of the model.  0 / -1. */
+int ptd_pool_load_ptk(pt_ctx *c, const ptd_ptk *f, int n, const char *const *ctab);
+
 /* ---- synthetic MB-iSTFT decoder (ref/v21_graph_trace.txt:3819-4065) ------------------------ *
  * 41 layers: 0 conv_pre, 1 ups.0, 2..19 MRF-256, 20 ups.1, 21..38 MRF-128, 39 conv_post, 40 the
  * final PQMF synthesis conv /dec/Conv (4 -> 1, K 63, packed [1][63][4][4]; bias may be NULL);
@@ -42,6 +72,9 @@ typedef struct ptd_model ptd_model;
  * table (closed-form Hann and irfft basis, layer 40's taps and bias).  Needs an initialised
  * context (its stream does the upload).  NULL on failure. */
 ptd_model *ptd_model_create(pt_ctx *c, const float *const *w, const float *const *b);
+/* The same model from a container's dec.* records (ptd_ptk_check_decoder must pass); fp16
+ * weights expand on the device.  The container may be closed after the call.  NULL on failure. */
+ptd_model *ptd_model_create_ptk(pt_ctx *c, const ptd_ptk *f);
 void ptd_model_destroy(ptd_model *m);
 
 /* Decode `batch` requests of T frames: z [batch][192][T] -> wav [batch][256*T].  Activations

@@ -48,6 +48,17 @@ _SIGS = {
     "pt_v21_dev_reclaim": (None, [VP]),
     "ptd_pool_load": (C.c_int, [VP, C.c_int, C.POINTER(VP), C.POINTER(C.c_size_t)]),
     "ptd_pool_record": (VP, [C.c_int]),
+    "ptd_ptk_open": (VP, [C.c_char_p]),
+    "ptd_ptk_close": (None, [VP]),
+    "ptd_ptk_count": (C.c_int, [VP]),
+    "ptd_ptk_find": (C.c_int, [VP, C.c_char_p]),
+    "ptd_ptk_info": (C.c_int, [VP, C.c_int, C.c_char_p, C.POINTER(C.c_int), C.POINTER(I64),
+                               C.POINTER(I64), C.POINTER(C.c_int)]),
+    "ptd_ptk_payload": (VP, [VP, C.c_int]),
+    "ptd_ptk_read_f32": (C.c_int, [VP, C.c_int, F, I64]),
+    "ptd_ptk_check_decoder": (C.c_int, [VP]),
+    "ptd_pool_load_ptk": (C.c_int, [VP, VP, C.c_int, C.POINTER(C.c_char_p)]),
+    "ptd_model_create_ptk": (VP, [VP, VP]),
     "ptd_model_create": (VP, [VP, C.POINTER(F), C.POINTER(F)]),
     "ptd_model_destroy": (None, [VP]),
     "ptd_decode": (C.c_int, [VP, VP, VP, I64, C.c_int, VP]),
@@ -216,8 +227,59 @@ class DevBuf:
             self.ptr = None
 
 
+class Ptk:
+    """A .ptk weight container opened by the library's reader (ptd_ptk_open)."""
+
+    def __init__(self, path):
+        self.lib = load()
+        self.ptr = self.lib.ptd_ptk_open(str(path).encode())
+        if not self.ptr:
+            raise ValueError(f"ptd_ptk_open refused {path}")
+
+    def __len__(self):
+        return self.lib.ptd_ptk_count(self.ptr)
+
+    def find(self, name: str) -> int:
+        return self.lib.ptd_ptk_find(self.ptr, name.encode())
+
+    def info(self, i: int):
+        """(name, shape, itemsize) of record i."""
+        name = C.create_string_buffer(65)
+        nd, isz = C.c_int(), C.c_int()
+        dims, nel = (I64 * 6)(), I64()
+        if self.lib.ptd_ptk_info(self.ptr, i, name, C.byref(nd), dims, C.byref(nel), C.byref(isz)):
+            raise IndexError(i)
+        return name.value.decode(), tuple(dims[:nd.value]), isz.value
+
+    def read(self, i: int) -> np.ndarray:
+        """Record i as float32 (fp16 payloads expanded by the library)."""
+        _, shape, _ = self.info(i)
+        out = np.empty(shape, np.float32)
+        if self.lib.ptd_ptk_read_f32(self.ptr, i, out.ctypes.data_as(F), out.size):
+            raise RuntimeError(f"ptd_ptk_read_f32({i}) failed")
+        return out
+
+    def check_decoder(self) -> bool:
+        return self.lib.ptd_ptk_check_decoder(self.ptr) == 0
+
+    def close(self):
+        if self.ptr:
+            self.lib.ptd_ptk_close(self.ptr)
+            self.ptr = None
+
+
 class Model:
-    """The synthetic decoder's weights on the device (ptd_model)."""
+    """The decoder's weights on the device (ptd_model): from packed arrays, or from a container
+    (Model.from_ptk)."""
+
+    @classmethod
+    def from_ptk(cls, ctx: Ctx, ptk: Ptk) -> "Model":
+        m = cls.__new__(cls)
+        m.lib = load()
+        m.ptr = m.lib.ptd_model_create_ptk(ctx.ptr, ptk.ptr)
+        if not m.ptr:
+            raise RuntimeError("ptd_model_create_ptk failed")
+        return m
 
     def __init__(self, ctx: Ctx, ws, bs):
         self.lib = load()

@@ -56,7 +56,7 @@ struct ptd_model {
   void *slab;                      /* relaid weights, biases, tail constants */
   const float *wr[PTD_DEC_NLAYER]; /* MFMA layout [Mp/32][K][cinp][32] */
   const float *b[PTD_DEC_NLAYER];
-  const float *consts;             /* hann, basis_c, basis_s, pqmf */
+  const float *consts;             /* the tail's table: hann, basis_c, basis_s, final conv */
   layer_geo g[PTD_DEC_NLAYER];
 };
 
@@ -86,45 +86,77 @@ static void tail_fir(float *dst, const float *wp, const float *bias) {
   dst[252] = bias ? bias[0] : 0.0f;
 }
 
-ptd_model *ptd_model_create(pt_ctx *c, const float *const *w, const float *const *b) {
+static void layer_gemm(const layer_geo *g, int *M, int *K) {
+  const int c4 = (g->cout + 3) / 4 * 4;
+  *M = g->convT ? g->sd * c4 : c4;
+  *K = g->convT ? (g->K + g->sd - 1) / g->sd : g->K;
+}
+
+int64_t ptdi_dec_wfloats(int i) {
+  if (i < 0 || i >= PTD_DEC_NLAYER) return -1;
+  const layer_geo g = dec_geo(i);
+  int M, K;
+  layer_gemm(&g, &M, &K);
+  return (int64_t) M * K * g.cin;
+}
+
+int ptdi_dec_cout(int i) { return i < 0 || i >= PTD_DEC_NLAYER ? -1 : dec_geo(i).cout; }
+
+ptd_model *ptdi_model_build(pt_ctx *c, const void *const *w, const int *wisz, const float *const *b) {
   if (!c || !c->use_cuda || !w || !b) return NULL;
   ptd_model *m = calloc(1, sizeof *m);
   if (!m) return NULL;
-  size_t total = 0, packed_max = 0;
-  size_t off_w[PTD_DEC_NLAYER], off_b[PTD_DEC_NLAYER], wbytes[PTD_DEC_NLAYER];
-  if (!w[PTD_DEC_NLAYER - 1]) {
-    PT_LOG("ptd_model_create: layer %d (the PQMF synthesis conv) has no weight", PTD_DEC_NLAYER - 1);
+  size_t total = 0, packed_max = 0, half_max = 0;
+  size_t off_w[PTD_DEC_NLAYER], off_b[PTD_DEC_NLAYER];
+  int64_t wn[PTD_DEC_NLAYER];
+  const int last = PTD_DEC_NLAYER - 1;
+  if (!w[last] || (wisz && wisz[last] != 4)) {
+    PT_LOG("decoder model: layer %d (the PQMF synthesis conv) needs an fp32 weight", last);
     free(m);
     return NULL;
   }
-  for (int i = 0; i < PTD_DEC_NLAYER - 1; i++) {
+  for (int i = 0; i < last; i++) {
+    const int isz = wisz ? wisz[i] : 4;
+    if (!w[i] || !b[i] || (isz != 4 && isz != 2)) {
+      PT_LOG("decoder model: layer %d has no weight or bias, or an item size other than 4 / 2", i);
+      free(m);
+      return NULL;
+    }
     layer_geo g = dec_geo(i);
     m->g[i] = g;
-    const int c4 = (g.cout + 3) / 4 * 4;
-    const int M = g.convT ? g.sd * c4 : c4, K = g.convT ? (g.K + g.sd - 1) / g.sd : g.K;
-    wbytes[i] = (size_t) M * K * g.cin * sizeof(float);
-    if (wbytes[i] > packed_max) packed_max = wbytes[i];
+    int M, K;
+    layer_gemm(&g, &M, &K);
+    wn[i] = (int64_t) M * K * g.cin;
+    if ((size_t) wn[i] * sizeof(float) > packed_max) packed_max = (size_t) wn[i] * sizeof(float);
+    if (isz == 2 && (size_t) wn[i] * 2 > half_max) half_max = (size_t) wn[i] * 2;
     off_w[i] = total;
     total += al256(ptk_relayout_floats(M, K, g.cin) * sizeof(float));
     off_b[i] = total;
     total += al256((size_t) g.cout * sizeof(float));
   }
-  m->g[PTD_DEC_NLAYER - 1] = dec_geo(PTD_DEC_NLAYER - 1);
+  m->g[last] = dec_geo(last);
   const size_t off_c = total;
   total += al256(PTK_TAIL_NCONST * sizeof(float));
   float consts[PTK_TAIL_NCONST];
   ptd_tail_constants(consts);
-  tail_fir(consts + PTD_TAIL_NCONST, w[PTD_DEC_NLAYER - 1], b[PTD_DEC_NLAYER - 1]);
-  void *tmp = NULL;
-  if (ptk_malloc(&m->slab, total) || ptk_malloc(&tmp, packed_max)) goto fail;
+  tail_fir(consts + PTD_TAIL_NCONST, (const float *) w[last], b[last]);
+  void *tmp = NULL, *tmp16 = NULL;
+  if (ptk_malloc(&m->slab, total) || ptk_malloc(&tmp, packed_max) ||
+      (half_max && ptk_malloc(&tmp16, half_max)))
+    goto fail;
   char *base = (char *) m->slab;
-  for (int i = 0; i < PTD_DEC_NLAYER - 1; i++) {
+  for (int i = 0; i < last; i++) {
     const layer_geo g = m->g[i];
-    const int c4 = (g.cout + 3) / 4 * 4;
-    const int M = g.convT ? g.sd * c4 : c4, K = g.convT ? (g.K + g.sd - 1) / g.sd : g.K;
-    /* the packed copy goes through one staging buffer; the stream orders reuse */
-    if (ptk_h2d_async(tmp, w[i], wbytes[i], c->g_stream) ||
-        ptk_relayout((float *) (base + off_w[i]), tmp, M, K, g.cin, c->g_stream) ||
+    int M, K;
+    layer_gemm(&g, &M, &K);
+    /* the packed copy goes through one staging buffer (fp16 payloads through a second one and
+     * the expansion kernel); the stream orders the reuse */
+    const int isz = wisz ? wisz[i] : 4;
+    const int up = isz == 4
+        ? ptk_h2d_async(tmp, w[i], (size_t) wn[i] * 4, c->g_stream)
+        : (ptk_h2d_async(tmp16, w[i], (size_t) wn[i] * 2, c->g_stream) ||
+           ptk_h2f((float *) tmp, (const uint16_t *) tmp16, wn[i], c->g_stream));
+    if (up || ptk_relayout((float *) (base + off_w[i]), tmp, M, K, g.cin, c->g_stream) ||
         ptk_h2d_async(base + off_b[i], b[i], (size_t) g.cout * sizeof(float), c->g_stream) ||
         ptk_stream_sync(c->g_stream))
       goto fail;
@@ -135,13 +167,19 @@ ptd_model *ptd_model_create(pt_ctx *c, const float *const *w, const float *const
     goto fail;
   m->consts = (const float *) (base + off_c);
   ptk_free(tmp);
+  ptk_free(tmp16);
   return m;
 fail:
-  PT_LOG("ptd_model_create failed: %s", ptk_last_error());
+  PT_LOG("decoder model creation failed: %s", ptk_last_error());
   ptk_free(tmp);
+  ptk_free(tmp16);
   ptk_free(m->slab);
   free(m);
   return NULL;
+}
+
+ptd_model *ptd_model_create(pt_ctx *c, const float *const *w, const float *const *b) {
+  return ptdi_model_build(c, (const void *const *) w, NULL, b);
 }
 
 void ptd_model_destroy(ptd_model *m) {

@@ -61,25 +61,33 @@ static struct {
   int n;
   char *slab;
   size_t slab_bytes, data_bytes;
-  size_t *off, *bytes;
+  size_t *off, *bytes;  /* device bytes (fp32) per record */
   const void **src;     /* host sources, for the claimed copies */
+  unsigned char *isz;   /* bytes per item of each source: 4 fp32, 2 fp16 (expanded on the device) */
+  size_t half_max;      /* largest fp16 source in bytes (staging size of a claimant) */
   volatile int next;    /* next record to claim */
   volatile int done;    /* records whose copy has COMPLETED (counted after a stream sync) */
   volatile int fail;
   relaid_t *rl;
-} P = {PTHREAD_MUTEX_INITIALIZER, 0, 0, 0, NULL, 0, 0, NULL, NULL, NULL, 0, 0, 0, NULL};
+} P = {PTHREAD_MUTEX_INITIALIZER, 0, 0, 0, NULL, 0, 0, NULL, NULL, NULL, NULL, 0, 0, 0, 0, NULL};
 
-/* lay the slab out and allocate it; called with P.lock held */
-static int pool_setup_locked(int n, const void *const *src, const size_t *bytes) {
+/* lay the slab out and allocate it; called with P.lock held.  bytes[i] is record i's size on
+ * the device (fp32); isz[i] the source's bytes per item (NULL: all 4) */
+static int pool_setup_locked(int n, const void *const *src, const size_t *bytes,
+                             const unsigned char *isz) {
   P.off = calloc((size_t) n, sizeof(size_t));
   P.bytes = calloc((size_t) n, sizeof(size_t));
   P.src = calloc((size_t) n, sizeof(void *));
+  P.isz = calloc((size_t) n, 1);
   P.rl = calloc((size_t) n, sizeof(relaid_t));
-  if (!P.off || !P.bytes || !P.src || !P.rl) goto oom;
+  if (!P.off || !P.bytes || !P.src || !P.isz || !P.rl) goto oom;
   size_t total = 0, data = 0;
+  P.half_max = 0;
   for (int i = 0; i < n; i++) {
     P.src[i] = src[i];
     P.bytes[i] = src[i] ? bytes[i] : 0;
+    P.isz[i] = isz ? isz[i] : 4;
+    if (P.isz[i] == 2 && P.bytes[i] / 2 > P.half_max) P.half_max = P.bytes[i] / 2;
     P.off[i] = total;
     total += (P.bytes[i] + 255) & ~(size_t) 255;
     data += P.bytes[i];
@@ -97,8 +105,8 @@ static int pool_setup_locked(int n, const void *const *src, const size_t *bytes)
   P.setup = 1;
   return 0;
 oom:
-  free(P.off); free(P.bytes); free(P.src); free(P.rl);
-  P.off = P.bytes = NULL; P.src = NULL; P.rl = NULL;
+  free(P.off); free(P.bytes); free(P.src); free(P.isz); free(P.rl);
+  P.off = P.bytes = NULL; P.src = NULL; P.isz = NULL; P.rl = NULL;
   return -1;
 }
 
@@ -107,14 +115,25 @@ oom:
  * enqueue) is what makes "done == n" mean the data is on the device. */
 static int pool_claim_upload(pt_ctx *c) {
   int mine = 0;
+  void *stage = NULL;   /* this claimant's fp16 staging buffer; the stream orders its reuse */
   for (;;) {
     const int i = __sync_fetch_and_add(&P.next, 1);
     if (i >= P.n) break;
-    if (P.bytes[i] && ptk_h2d_async(P.slab + P.off[i], P.src[i], P.bytes[i], c->g_stream))
-      __sync_bool_compare_and_swap(&P.fail, 0, 1);
     mine++;
+    if (!P.bytes[i]) continue;
+    int bad;
+    if (P.isz[i] == 4) {
+      bad = ptk_h2d_async(P.slab + P.off[i], P.src[i], P.bytes[i], c->g_stream);
+    } else {
+      const int64_t items = (int64_t) (P.bytes[i] / 4);
+      bad = (!stage && ptk_malloc(&stage, P.half_max)) ||
+            ptk_h2d_async(stage, P.src[i], (size_t) items * 2, c->g_stream) ||
+            ptk_h2f((float *) (P.slab + P.off[i]), (const uint16_t *) stage, items, c->g_stream);
+    }
+    if (bad) __sync_bool_compare_and_swap(&P.fail, 0, 1);
   }
   if (mine && ptk_stream_sync(c->g_stream)) __sync_bool_compare_and_swap(&P.fail, 0, 1);
+  ptk_free(stage);
   __sync_fetch_and_add(&P.done, mine);
   while (__sync_add_and_fetch(&P.done, 0) < P.n && !__sync_add_and_fetch(&P.fail, 0)) sched_yield();
   if (P.fail) {
@@ -128,8 +147,8 @@ static void pool_free_locked(void) {
   if (P.rl)
     for (int i = 0; i < P.n; i++) ptk_free(P.rl[i].dev);
   ptk_free(P.slab);
-  free(P.off); free(P.bytes); free(P.src); free(P.rl);
-  P.slab = NULL; P.off = P.bytes = NULL; P.src = NULL; P.rl = NULL;
+  free(P.off); free(P.bytes); free(P.src); free(P.isz); free(P.rl);
+  P.slab = NULL; P.off = P.bytes = NULL; P.src = NULL; P.isz = NULL; P.rl = NULL;
   P.n = 0; P.setup = 0; P.slab_bytes = P.data_bytes = 0;
 }
 
@@ -143,7 +162,8 @@ void ptdi_pool_ref(int delta) {
   pthread_mutex_unlock(&P.lock);
 }
 
-int ptd_pool_load(pt_ctx *c, int n, const void *const *host, const size_t *bytes) {
+int ptdi_pool_load_src(pt_ctx *c, int n, const void *const *host, const size_t *bytes,
+                       const unsigned char *isz) {
   if (!c || !c->use_cuda || n <= 0) return -1;
   pthread_mutex_lock(&P.lock);
   int r = 0;
@@ -151,11 +171,15 @@ int ptd_pool_load(pt_ctx *c, int n, const void *const *host, const size_t *bytes
     PT_LOG("weight pool already holds %d records (asked to load %d)", P.n, n);
     r = -1;
   } else if (!P.setup) {
-    r = pool_setup_locked(n, host, bytes);
+    r = pool_setup_locked(n, host, bytes, isz);
   }
   pthread_mutex_unlock(&P.lock);
   if (r) return -1;
   return pool_claim_upload(c);
+}
+
+int ptd_pool_load(pt_ctx *c, int n, const void *const *host, const size_t *bytes) {
+  return ptdi_pool_load_src(c, n, host, bytes, NULL);
 }
 
 const void *ptdi_pool_get(int idx, size_t need) {
@@ -280,7 +304,7 @@ int ptdi_ctx_init(pt_ctx *c, size_t arena_bytes, int verbose) {
       src[i] = pt_v21_cont(c, i);
       nb[i] = src[i] ? pt_v21_cont_bytes(c, i) : 0;
     }
-    if (r == 0 && n > 0) r = pool_setup_locked(n, src, nb);
+    if (r == 0 && n > 0) r = pool_setup_locked(n, src, nb, NULL);
     free(src);
     free(nb);
   }

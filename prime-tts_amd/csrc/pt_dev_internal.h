@@ -3,6 +3,7 @@
 #define PT_DEV_INTERNAL_H_
 
 #include <stddef.h>
+#include <stdint.h>
 #include <stdio.h>
 
 #include "pt_v21_dev.h"
@@ -25,6 +26,11 @@ const void *ptdi_pool_get(int idx, size_t need);
 /* relaid MFMA copy of pool record idx for (M rows, K taps, cin), built once per process on the
  * caller's stream; NULL when idx is not resident */
 const float *ptdi_pool_relaid(pt_ctx *c, int idx, int M, int K, int cin);
+/* set the pool up from n host records (when empty) and upload the share this context claims:
+ * bytes[i] = record i's fp32 size on the device, isz[i] = its source's bytes per item (4, or 2
+ * for fp16 sources expanded on the device; NULL = all 4).  Sources must stay valid until return. */
+int ptdi_pool_load_src(pt_ctx *c, int n, const void *const *host, const size_t *bytes,
+                       const unsigned char *isz);
 /* take / drop a reference on the pool (init / shutdown) */
 void ptdi_pool_ref(int delta);
 
@@ -40,6 +46,15 @@ void ptdi_conv_desc(ptk_conv_desc *d, const float *x, int64_t ldx, int64_t bsx, 
 int64_t ptdi_convT_desc(ptk_conv_desc *d, const float *x, int64_t ldx, int64_t bsx, int64_t tin,
                         int cin, const float *wr, const float *bias, int cout, int s, int pad,
                         int K, float *y, int64_t ldy, int64_t bsy, int batch);
+
+/* decoder layer i's packed weight size in floats (conv [C4/4][K][cin][4]; convT phase rows
+ * [s*C4/4][ceil(K/s)][cin][4]) and its output channel count; -1 outside 0..PTD_DEC_NLAYER-1 */
+int64_t ptdi_dec_wfloats(int i);
+int ptdi_dec_cout(int i);
+/* the decoder model from per-layer host sources: w[i] packed, wisz[i] bytes per item (4 fp32, 2
+ * fp16 expanded on the device; wisz NULL = all fp32); the final conv's weight must be fp32 */
+struct ptd_model *ptdi_model_build(pt_ctx *c, const void *const *w, const int *wisz,
+                                   const float *const *b);
 
 /* pt_v21_cuda_init with an explicit arena size */
 int ptdi_ctx_init(pt_ctx *c, size_t arena_bytes, int verbose);

@@ -106,6 +106,9 @@ typedef struct {
 int ptk_conv_cinp(int cin);
 size_t ptk_relayout_floats(int M, int K, int cin);
 int ptk_relayout(float *dst, const float *wp, int M, int K, int cin, void *s);
+/* fp16 -> fp32 expansion of n items (bit-exact: subnormals keep their value, inf / NaN keep sign
+ * and payload, nothing is quieted) */
+int ptk_h2f(float *dst, const uint16_t *src, int64_t n, void *s);
 
 /* Launch ngroup independent problems (1..PTK_MAX_GROUP) in one grid; heavy problems first.
  * Returns 0, or -1 when a shape is outside what the kernels support (ptk_last_error says why). */

@@ -199,6 +199,37 @@ extern "C" int ptk_relayout(float *dst, const float *wp, int M, int K, int cin, 
   return 0;
 }
 
+// ------------------------------------------------------------------------------ fp16 expansion
+// binary16 -> binary32 by its bit fields.  Every binary16 value is exact in binary32: normals
+// rebias the exponent (15 -> 127), subnormals m * 2^-24 renormalise around their leading one,
+// inf / NaN keep sign and payload.  Integer work only, so no float mode (denormal flushing,
+// NaN quieting) can change a result.
+__device__ __forceinline__ unsigned half_to_float_bits(unsigned h) {
+  const unsigned s = (h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  if (e == 31u) return s | 0x7f800000u | (m << 13);
+  if (e != 0u) return s | ((e + 112u) << 23) | (m << 13);
+  if (m == 0u) return s;
+  const unsigned p = 31u - (unsigned) __builtin_clz(m);   // leading one at bit p (0..9)
+  return s | ((p + 103u) << 23) | ((m << (23u - p)) & 0x7fffffu);
+}
+
+__global__ void h2f_kernel(float *__restrict__ dst, const unsigned short *__restrict__ src,
+                           long long n) {
+  const long long st = (long long) gridDim.x * blockDim.x;
+  for (long long i = (long long) blockIdx.x * blockDim.x + threadIdx.x; i < n; i += st)
+    dst[i] = __uint_as_float(half_to_float_bits(src[i]));
+}
+
+extern "C" int ptk_h2f(float *dst, const uint16_t *src, int64_t n, void *s) {
+  if (n <= 0) return 0;
+  long long blocks = (n + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(h2f_kernel, dim3((unsigned) blocks), dim3(256), 0, (hipStream_t) s, dst,
+                     (const unsigned short *) src, (long long) n);
+  HCHK(hipGetLastError());
+  return 0;
+}
+
 // ------------------------------------------------------------------------------ epilogue
 __device__ __forceinline__ float epi_apply(float v, const ptk_epi &e, int b, int co, long long col) {
   switch (e.op) {

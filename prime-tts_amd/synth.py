@@ -91,6 +91,33 @@ def dec_layer(i: int) -> dict:
     return dict(cin=C, cout=C, K=K, s=1, d=d, pad=d * (K - 1) // 2, convT=False)
 
 
+def layer_module(i: int) -> str:
+    """Container module name of decoder layer i (its records are <module>.wp[#h] and <module>.b;
+    spec/v21_layers.json, the dec.* packed records)."""
+    fixed = {0: "dec.conv_pre", 1: "dec.ups.0", 20: "dec.ups.1", 39: "dec.subband_conv_post",
+             40: "dec.Conv"}
+    if i in fixed:
+        return fixed[i]
+    base = 2 if i < 20 else 21
+    o = i - base
+    return f"dec.resblocks.{o // 6 + (0 if i < 20 else 3)}.convs{o % 2 + 1}.{(o % 6) // 2}"
+
+
+def tail_convT_weights():
+    """ONNX weights [Cin][Cout][K] of the decoder's three fixed tail convTs (stride 4): iSTFT
+    overlap-add 16 -> 1 with the delta kernel, window-sum 1 -> 1 with the squared periodic
+    Hann(16), PQMF zero-insert 4 -> 4 with 4 at tap 0 (ref/v21_graph_trace.txt:3616-3617,
+    :4044-4046)."""
+    ola = np.zeros((16, 1, 16), np.float32)
+    ola[np.arange(16), 0, np.arange(16)] = 1.0
+    n = np.arange(16)
+    hann = 0.5 - 0.5 * np.cos(2 * np.pi * n / 16)
+    wsum = (hann * hann).astype(np.float32).reshape(1, 1, 16)
+    up = np.zeros((4, 4, 4), np.float32)
+    up[np.arange(4), np.arange(4), 0] = 4.0
+    return {"dec.ConvTranspose": ola, "dec.ConvTranspose_1": wsum, "dec.ConvTranspose_2": up}
+
+
 def conv_weights(rng: np.random.Generator, cin: int, cout: int, K: int):
     W = rng.standard_normal((cout, cin, K), dtype=np.float64) * np.sqrt(1.0 / (cin * K))
     b = rng.standard_normal(cout, dtype=np.float64) * 0.1
