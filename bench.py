@@ -21,6 +21,7 @@ import importlib.util
 import json
 import os
 import pathlib
+import re
 import sys
 import time
 
@@ -41,6 +42,21 @@ def _package():
     sys.modules["prime_tts_amd"] = mod
     spec.loader.exec_module(mod)
     return mod
+
+
+PROFILE_DOMINANT = ROOT / "profiles" / "conv_mfma_mrf256_group_T904.md"
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel, as the committed rocprofv3 summary states them
+    (FETCH_SIZE and WRITE_SIZE passes over `bench.py --kernel-loop`, scaled by the copy-kernel
+    calibration); None when the summary is absent."""
+    try:
+        text = PROFILE_DOMINANT.read_text()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", text, re.M)
+    return int(m.group(1)) if m else None
 
 
 def log(msg):
@@ -85,20 +101,36 @@ def mrf_depth_setup(pkg, ctx, stage, T):
 
 def cpu_baseline(pkg):
     """The reference's own CPU conv path (oracle/_ref, built from the reference sources) inside the
-    oracle's decoder driver, or the C restatement when _ref is absent: one config-4 request."""
+    oracle's decoder driver, or the C restatement when _ref is absent.  Timed two ways: config 5's
+    eight requests as eight host threads pinned to eight distinct cores (the reference's
+    one-thread-per-stream model, main_v21_par.c:134-140), and one config-4 request on one thread."""
     sys.path.insert(0, str(ROOT / "tests"))
     import oracle_lib as ol
-    T = 226
     ws, bs = pkg.synth.decoder_weights(1234)
-    z = pkg.synth.latent(T, 226)
     kind = "reference" if ol.have_ref() else "port"
+    use_ref = kind == "reference"
+    cores = sorted(os.sched_getaffinity(0))
+    # eight requests of config 5 (the long-form request is left out of the CPU sample)
+    Ts = pkg.synth.request_lengths(5, 8)
+    zs = [pkg.synth.latent(T, 900 + i) for i, T in enumerate(Ts)]
+    nthr = min(8, len(cores))
+    _, dt8 = ol.decoder_threads(ws, bs, zs, cores[:nthr], use_ref=use_ref)
+    audio8 = sum(Ts) * HOP / SR
+    # one config-4 request on one thread
+    T = 226
+    z = pkg.synth.latent(T, 226)
     t0 = time.perf_counter()
-    ol.decoder(ws, bs, z, use_ref=kind == "reference")
-    dt = time.perf_counter() - t0
-    audio = T * HOP / SR
-    return {"value": round(audio / dt, 4), "unit": "audio-s/s", "cores": 1, "kind": kind,
-            "sample": f"one config-4 decode (T=226, {audio:.3f} s audio) on 1 host thread: {dt:.2f} s",
-            "model": _cpu_model()}
+    ol.decoder(ws, bs, z, use_ref=use_ref)
+    dt1 = time.perf_counter() - t0
+    audio1 = T * HOP / SR
+    return {"value": round(audio8 / dt8, 4), "unit": "audio-s/s", "cores": nthr, "kind": kind,
+            "sample": f"config 5's 8 requests (T={Ts}, {audio8:.2f} s audio; the T=1500 long-form "
+                      f"request not included) as {nthr} threads pinned to cores {cores[:nthr]}: "
+                      f"{dt8:.2f} s wall",
+            "single_thread": {"value": round(audio1 / dt1, 4), "unit": "audio-s/s", "cores": 1,
+                              "sample": f"one config-4 decode (T=226, {audio1:.3f} s audio) on 1 "
+                                        f"thread: {dt1:.2f} s"},
+            "host_cpus": len(cores), "model": _cpu_model()}
 
 
 def _cpu_model():
@@ -256,14 +288,15 @@ def main():
             "kernel": "conv_mfma_kernel (MRF-256 grouped launch: 3 branch convs K 3/7/11, C 256, T 904)",
             "bound": "mfma", "achieved": round(achieved, 3), "peak": MFMA_F32_PEAK,
             "unit": "TFLOP/s", "frac": round(achieved / MFMA_F32_PEAK, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
+            "traffic_source": str(PROFILE_DOMINANT.relative_to(ROOT)),
             "flop_per_launch": flop_launch, "alg_bytes_per_launch": bytes_launch,
             "us_per_launch": round(ms_launch * 1e3, 3),
         },
         **cfg,
     }
     if not args.no_cpu_baseline:
-        log("cpu baseline (reference conv path, 1 thread) ...")
+        log("cpu baseline (reference conv path: 8 pinned threads, then 1 thread) ...")
         out["cpu_baseline"] = cpu_baseline(pkg)
     timer.close()
     model.close()

@@ -146,6 +146,45 @@ def decoder(ws, bs, z, stages=False, use_ref=False):
     return (wav, bufs) if stages else wav
 
 
+def decoder_threads(ws, bs, zs, cores, use_ref=False):
+    """Decode the requests zs concurrently, one host thread per request, thread i pinned to
+    cores[i % len(cores)] (the reference's one-thread-per-stream model, main_v21_par.c:134-140).
+    The conv implementation is chosen once for all threads.  Returns (waveforms, wall seconds)."""
+    import os
+    import threading
+    import time
+    lib = oracle()
+    if use_ref:
+        r = ref()
+        lib.orc_set_conv_impl(C.cast(r.ref_conv_cpu, C.c_void_p), C.cast(r.ref_convT_cpu, C.c_void_p))
+    st = dec_weights_struct(ws, bs)
+    zs = [np.ascontiguousarray(z, np.float32) for z in zs]
+    wavs = [np.zeros(256 * z.shape[-1], np.float32) for z in zs]
+    rcs = [None] * len(zs)
+    start = threading.Barrier(len(zs) + 1)
+
+    def work(i):
+        os.sched_setaffinity(0, {cores[i % len(cores)]})   # 0 = the calling thread on Linux
+        start.wait()
+        rcs[i] = lib.orc_decoder(C.byref(st), fptr(zs[i]), zs[i].shape[-1], fptr(wavs[i]),
+                                 C.POINTER(F)())
+
+    ts = [threading.Thread(target=work, args=(i,)) for i in range(len(zs))]
+    try:
+        for t in ts:
+            t.start()
+        start.wait()
+        t0 = time.perf_counter()
+        for t in ts:
+            t.join()
+        dt = time.perf_counter() - t0
+    finally:
+        if use_ref:
+            lib.orc_set_conv_impl(None, None)
+    assert all(rc == 0 for rc in rcs), rcs
+    return wavs, dt
+
+
 def mrf(wts, bts, x, alpha):
     lib = oracle()
     C_, T = x.shape

@@ -266,3 +266,16 @@ def test_decoder_mutation_caught():
     ref, mid = np_ref.decoder(raw, bs, z)
     m0_bad = np_ref.leaky(3.0 * np_ref.mrf(raw[2:20], bs[2:20], mid["x0"], 0.1), 0.1)
     assert rel(m0_bad, mid["m0"]) > 1e-2
+
+
+def test_decoder_threads_match_single():
+    """The threaded driver bench.py's CPU baseline uses gives each request exactly its
+    single-threaded decode."""
+    import os
+    ws, bs = synth.decoder_weights(31)
+    zs = [synth.latent(T, 40 + T) for T in (9, 14, 11)]
+    cores = sorted(os.sched_getaffinity(0))[:2]
+    for use_ref in ([False, True] if ol.have_ref() else [False]):
+        wavs, _ = ol.decoder_threads(ws, bs, zs, cores, use_ref=use_ref)
+        for z, w in zip(zs, wavs):
+            assert np.array_equal(w, ol.decoder(ws, bs, z, use_ref=use_ref))
