@@ -652,8 +652,12 @@ int pt_v21_matmul(pt_ctx *c, const float *A, int64_t m, int64_t k, int64_t lda, 
     PT_LOG("pt_v21_matmul: bad arguments");
     return -1;
   }
-  const size_t ab = (size_t) m * lda * sizeof(float), bb = (size_t) (k > 0 ? k : 1) * ldb * sizeof(float);
-  const size_t cb = (size_t) m * ldc * sizeof(float);
+  /* tight device copies: only the k (A), n (B, C) columns each row uses are moved, so no byte
+   * outside the matrices is read, and C's padding columns (ldc > n) are left as they are, as the
+   * reference's CPU matmul leaves them (pt_v21_host.c:2635-2650) */
+  const size_t ab = (size_t) m * (k > 0 ? k : 1) * sizeof(float);
+  const size_t bb = (size_t) (k > 0 ? k : 1) * nn * sizeof(float);
+  const size_t cb = (size_t) m * nn * sizeof(float);
   void *mark = ptdi_arena_mark(c);
   float *dA = ptdi_arena_alloc(c, ab), *dB = ptdi_arena_alloc(c, bb), *dC = ptdi_arena_alloc(c, cb);
   int own = 0;
@@ -667,10 +671,12 @@ int pt_v21_matmul(pt_ctx *c, const float *A, int64_t m, int64_t k, int64_t lda, 
     }
     own = 1;
   }
-  int r = ptk_h2d_async(dA, A, ab, c->g_stream) ||
-          (k > 0 && ptk_h2d_async(dB, B, (size_t) k * ldb * sizeof(float), c->g_stream)) ||
-          ptk_matmul(dA, m, k, lda, dB, ldb, nn, dC, ldc, c->g_stream) || ptdi_wait(c) ||
-          ptk_d2h_async(C, dC, cb, c->g_stream) || ptk_stream_sync(c->g_stream);
+  const size_t f = sizeof(float);
+  int r = (k > 0 && (ptk_h2d_2d_async(dA, (size_t) k * f, A, (size_t) lda * f, (size_t) k * f, (size_t) m, c->g_stream) ||
+                     ptk_h2d_2d_async(dB, (size_t) nn * f, B, (size_t) ldb * f, (size_t) nn * f, (size_t) k, c->g_stream))) ||
+          ptk_matmul(dA, m, k, k, dB, nn, nn, dC, nn, c->g_stream) || ptdi_wait(c) ||
+          ptk_d2h_2d_async(C, (size_t) ldc * f, dC, (size_t) nn * f, (size_t) nn * f, (size_t) m, c->g_stream) ||
+          ptk_stream_sync(c->g_stream);
   if (r) PT_LOG("pt_v21_matmul failed: %s", ptk_last_error());
   if (own) {
     ptk_free(dA); ptk_free(dB); ptk_free(dC);

@@ -757,25 +757,53 @@ extern "C" int ptk_convT_simt(const float *x, int64_t ldx, int64_t bsx, int64_t 
 }
 
 // ------------------------------------------------------------------------------ matmul
-__global__ void matmul_kernel(const float *__restrict__ A, long long m, long long k, long long lda,
-                              const float *__restrict__ B, long long ldb, long long nn,
-                              float *__restrict__ C, long long ldc) {
-  const long long j = (long long) blockIdx.x * blockDim.x + threadIdx.x;
-  const long long i = blockIdx.y;
-  if (j >= nn || i >= m) return;
-  const float *ar = A + i * lda;
-  float v = 0.0f;
-  for (long long p = 0; p < k; p++) v += ar[p] * B[p * ldb + j];
-  C[i * ldc + j] = v;
+// fp32 MFMA matmul, C[m][n] = A[m][k] . B[k][n], all row-major with leading dimensions lda, ldb,
+// ldc (the reference's pt_v21_matmul contract).  A workgroup computes a 64x64 block of C, each of
+// its four waves a 32x32 tile, walking k in steps of 8: lane (h, r) feeds A[row r][k0 + 2p + h]
+// and B[k0 + 2p + h][column r] to the p-th of four v_mfma_f32_32x32x2_f32 (the operand layout of
+// the conv kernel).  Loads outside the matrices read as 0, so any m, n, k works.
+__global__ void __launch_bounds__(256) matmul_mfma_kernel(const float *__restrict__ A, long long m,
+                                                          long long k, long long lda,
+                                                          const float *__restrict__ B,
+                                                          long long ldb, long long nn,
+                                                          float *__restrict__ C, long long ldc) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  const long long r0 = (long long) blockIdx.y * 64 + (w >> 1) * 32;
+  const long long c0 = (long long) blockIdx.x * 64 + (w & 1) * 32;
+  const long long ra = r0 + l32, cb = c0 + l32;
+  const bool rok = ra < m, cok = cb < nn;
+  const float *arow = A + (rok ? ra : 0) * lda;
+  f32x16 acc;
+#pragma unroll
+  for (int v = 0; v < 16; v++) acc[v] = 0.0f;
+  for (long long k0 = 0; k0 < k; k0 += 8) {
+    float av[4], bv[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const long long kk = k0 + 2 * q + h;
+      const bool kok = kk < k;
+      av[q] = (rok && kok) ? arow[kk] : 0.0f;
+      bv[q] = (cok && kok) ? B[kk * ldb + cb] : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q], bv[q], acc, 0, 0, 0);
+  }
+#pragma unroll
+  for (int v = 0; v < 16; v++) {
+    const long long row = r0 + 8 * (v >> 2) + 4 * h + (v & 3);
+    if (row < m && cok) C[row * ldc + cb] = acc[v];
+  }
 }
 extern "C" int ptk_matmul(const float *A, int64_t m, int64_t k, int64_t lda, const float *B,
                           int64_t ldb, int64_t nn, float *C, int64_t ldc, void *s) {
   if (m <= 0 || nn <= 0) return 0;
-  if (m > 65535) {
-    set_err("ptk_matmul: m %lld above the grid limit", (long long) m);
+  const long long gy = (m + 63) / 64, gx = (nn + 63) / 64;
+  if (gy > 65535 || gx > 0x7fffffffLL) {
+    set_err("ptk_matmul: %lld x %lld outside the grid limits", (long long) m, (long long) nn);
     return -1;
   }
-  hipLaunchKernelGGL(matmul_kernel, dim3((unsigned) ((nn + 255) / 256), (unsigned) m), dim3(256), 0,
+  hipLaunchKernelGGL(matmul_mfma_kernel, dim3((unsigned) gx, (unsigned) gy), dim3(256), 0,
                      (hipStream_t) s, A, (long long) m, (long long) k, (long long) lda, B,
                      (long long) ldb, (long long) nn, C, (long long) ldc);
   HCHK(hipGetLastError());

@@ -131,6 +131,13 @@ WIDE_CONV = [  # batch, cin, cout, T, K, stride, pad, dil, epi0, epi1  (MFMA pat
     (2, 64, 40, 97, 5, 2, 2, 1, 2, 3),         # stride 2, batch 2, cout not a multiple of 32
     (3, 33, 20, 45, 3, 1, 1, 2, 4, 1),         # odd cin, batch 3
     (1, 16, 16, 40, 1, 1, 0, 1, 0, 0),         # K = 1
+    # the other graphs' convs (spec/v21_layers.json: enc, dp, flow), all through the same ABI
+    (1, 192, 768, 120, 3, 1, 0, 1, 2, 0),      # enc FFN conv 1 + ReLU
+    (1, 768, 192, 120, 3, 1, 0, 1, 3, 0),      # enc FFN conv 2 + mask multiply
+    (1, 192, 384, 150, 5, 1, 2, 1, 0, 0),      # flow WN in-layer, K 5
+    (1, 256, 1536, 64, 1, 1, 0, 1, 0, 0),      # flow 256 -> 1536 projection
+    (1, 192, 96, 150, 1, 1, 0, 1, 3, 0),       # flow post, K 1 + multiply
+    (1, 256, 1, 90, 1, 1, 0, 1, 3, 0),         # dp projection to one channel (SIMT path)
 ]
 
 
@@ -251,15 +258,25 @@ def test_pool_resident_weights(ctx):
     assert np.array_equal(y_small, y_call)
 
 
-def test_matmul(ctx):
-    say("matmul")
-    rng = np.random.default_rng(3)
-    A = rng.standard_normal((37, 53)).astype(np.float32)
-    B = rng.standard_normal((53, 29)).astype(np.float32)
-    Cm = np.zeros((37, 29), np.float32)
-    assert ctx.lib.pt_v21_matmul(ctx.ptr, pkg.fptr(A), 37, 53, 53, pkg.fptr(B), 29, 29,
-                                 pkg.fptr(Cm), 29) == 0
-    assert relerr(Cm, A.astype(np.float64) @ B) < 1e-5
+@pytest.mark.parametrize("m,k,n,pad", [(37, 53, 29, 0), (120, 192, 120, 0), (120, 96, 192, 0),
+                                       (70, 13, 65, 3), (5, 0, 7, 1)])
+def test_matmul(ctx, m, k, n, pad):
+    """pt_v21_matmul (fp32 MFMA) against float64, with tight and padded leading dimensions
+    (lda = k + pad, ldb = ldc = n + pad) and the k = 0 case (C = 0)."""
+    say(f"matmul {m}x{k}x{n} pad {pad}")
+    rng = np.random.default_rng(3 + m)
+    lda, ldb, ldc = k + pad, n + pad, n + pad
+    Af = rng.standard_normal((m, max(lda, 1))).astype(np.float32)
+    Bf = rng.standard_normal((max(k, 1), ldb)).astype(np.float32)
+    Cf = np.full((m, ldc), 7.0, np.float32)
+    assert ctx.lib.pt_v21_matmul(ctx.ptr, pkg.fptr(Af), m, k, lda, pkg.fptr(Bf), ldb, n,
+                                 pkg.fptr(Cf), ldc) == 0
+    ref = Af[:, :k].astype(np.float64) @ Bf[:k, :n]
+    if k == 0:
+        assert np.all(Cf[:, :n] == 0.0)
+    else:
+        assert relerr(Cf[:, :n], ref) < 1e-5
+    assert np.all(Cf[:, n:] == 7.0)   # columns past n untouched
 
 
 def test_device_residency(ctx):
