@@ -11,7 +11,8 @@ fp32-MFMA roofline (HIP events on the stream it runs on), and the reference's CP
 on this host on a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-       python bench.py --kernel-loop N   (only the dominant kernel, N launches: for rocprofv3 --pmc)
+       python bench.py --kernel-loop N   (only the dominant kernel and the tail kernel, N launches
+                                          each: for rocprofv3 --pmc)
 """
 from __future__ import annotations
 
@@ -99,6 +100,21 @@ def mrf_depth_setup(pkg, ctx, stage, T):
     return xs + xls + a_s + ys, arr(xs), arr(xls), arr(a_s), arr(ys)
 
 
+TAIL_L = 16 * 226 + 1   # conv_post frames of a T = 226 request
+
+
+def tail_setup(pkg, ctx, L, batch):
+    """conv_post-shaped input [batch][72][L] (log-magnitudes and phase logits ~ N(0, 0.5)) and the
+    waveform buffer for ptd_tail."""
+    p = (0.7 * np.random.default_rng(9).standard_normal((batch, 72, L))).astype(np.float32)
+    return pkg.DevBuf.of(ctx, p), pkg.DevBuf(batch * 16 * (L - 1))
+
+
+def tail_bytes(L, batch):
+    """Algorithmic HBM bytes of one tail launch: read conv_post's 72 rows, write the waveform."""
+    return 4.0 * batch * (72 * L + 16 * (L - 1))
+
+
 def cpu_baseline(pkg):
     """The reference's own CPU conv path (oracle/_ref, built from the reference sources) inside the
     oracle's decoder driver, or the C restatement when _ref is absent.  Timed two ways: config 5's
@@ -174,6 +190,13 @@ def main():
                 raise RuntimeError("mrf depth failed")
         ctx.sync()
         log(f"kernel loop: {2 * args.kernel_loop} launches done")
+        # the narrow late stages: the fused tail kernel at config 4's shape, as many launches
+        tp, tw = tail_setup(pkg, ctx, TAIL_L, 1)
+        for _ in range(args.kernel_loop):
+            if lib.ptd_tail(ctx.ptr, model.ptr, tp.ptr, TAIL_L, 1, tw.ptr) != 0:
+                raise RuntimeError("tail failed")
+        ctx.sync()
+        log(f"kernel loop: {args.kernel_loop} tail launches (L {TAIL_L}) done")
         # calibration for the HBM byte counters: add_kernel over 64 Mi floats reads exactly
         # 512 MiB and writes 256 MiB per launch
         n = 64 << 20
@@ -194,6 +217,18 @@ def main():
     for b in bufs:
         b.free()
     log(f"dominant kernel: MRF-256 grouped conv {ms_launch * 1e3:.1f} us/launch = {achieved:.2f} TFLOP/s")
+
+    # ---------------------------------------------------------------- narrow late stages (GB/s)
+    tail = {}
+    for batch in (1, 8):
+        tp, tw = tail_setup(pkg, ctx, TAIL_L, batch)
+        ft = lambda: lib.ptd_tail(ctx.ptr, model.ptr, tp.ptr, TAIL_L, batch, tw.ptr)  # noqa: E731
+        ft()
+        ms = timer.time(ft, 50)
+        tail[f"batch{batch}"] = {"us": round(ms * 1e3, 2),
+                                 "gbps": round(tail_bytes(TAIL_L, batch) / (ms * 1e-3) / 1e9, 1)}
+        tp.free(); tw.free()
+    log(f"tail kernel (iSTFT + PQMF, L {TAIL_L}): {tail}")
 
     # ---------------------------------------------------------------- configs 1-3 (TFLOP/s)
     cfg = {}
@@ -292,6 +327,12 @@ def main():
             "traffic_source": str(PROFILE_DOMINANT.relative_to(ROOT)),
             "flop_per_launch": flop_launch, "alg_bytes_per_launch": bytes_launch,
             "us_per_launch": round(ms_launch * 1e3, 3),
+        },
+        "narrow_stages": {
+            "kernel": f"tail_kernel (iSTFT + PQMF synthesis fused; conv_post output [72][{TAIL_L}] "
+                      f"-> {16 * (TAIL_L - 1)} samples per request)",
+            "bound": "hbm", "peak_gbps": HBM_PEAK,
+            "alg_bytes_per_request": tail_bytes(TAIL_L, 1), **tail,
         },
         **cfg,
     }

@@ -88,6 +88,13 @@ size_t ptd_decode_arena_bytes(int64_t T, int batch);
 int ptd_decode_stages(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, float *wav,
                       float *const *stages);
 
+/* The decoder tail alone, the stages after conv_post (ref/v21_graph_trace.txt:4176-4315): p is
+ * conv_post's output [batch][72][L] (4 subbands x (9 log-magnitudes + 9 phase logits)), wav gets
+ * [batch][16*(L-1)] samples: exp / sin / cos -> irfft (n_fft 16) -> Hann -> overlap-add (hop 4)
+ * -> window-sum normalisation -> [8:-8] trim -> PQMF x4 zero-insert -> the model's 63-tap
+ * synthesis conv (layer 40).  One kernel, asynchronous.  0 / -1. */
+int ptd_tail(pt_ctx *c, const ptd_model *m, const float *p, int64_t L, int batch, float *wav);
+
 /* Run decoder layer i (0..39) alone: conv (x [batch][cin][T] -> y [batch][cout4][Tout]) or convT
  * (x [batch][cin][T] -> y [batch][cout4][Lout]).  in_leaky > 0 applies LeakyReLU(in_leaky) to
  * the input as it is read; epi_leaky > 0 applies it to the output.  Asynchronous. */

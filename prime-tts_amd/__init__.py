@@ -65,6 +65,7 @@ _SIGS = {
     "ptd_decode_arena_bytes": (C.c_size_t, [I64, C.c_int]),
     "ptd_decode_stages": (C.c_int, [VP, VP, VP, I64, VP, C.POINTER(VP)]),
     "ptd_layer": (C.c_int, [VP, VP, C.c_int, VP, I64, C.c_int, VP, C.c_float, C.c_float]),
+    "ptd_tail": (C.c_int, [VP, VP, VP, I64, C.c_int, VP]),
     "ptd_mrf": (C.c_int, [VP, VP, C.c_int, VP, I64, C.c_float, VP]),
     "ptd_mrf_depth": (C.c_int, [VP, VP, C.c_int, C.c_int, C.POINTER(VP), C.POINTER(VP),
                                 C.POINTER(VP), C.POINTER(VP), C.POINTER(VP), I64]),

@@ -271,6 +271,15 @@ static int mrf_run(pt_ctx *c, const ptd_model *m, int stage, const float *x, con
   return mrf_depth(c, m, stage, 2, p2, l1, a, out, NULL, T, batch);
 }
 
+int ptd_tail(pt_ctx *c, const ptd_model *m, const float *p, int64_t L, int batch, float *wav) {
+  if (!c || !c->use_cuda || !m || !p || !wav || L < 2 || batch < 1) return -1;
+  if (ptk_tail_batched(p, L, 72 * L, L, wav, 16 * (L - 1), batch, m->consts, NULL, c->g_stream)) {
+    PT_LOG("ptd_tail failed: %s", ptk_last_error());
+    return -1;
+  }
+  return 0;
+}
+
 size_t ptd_decode_arena_bytes(int64_t T, int batch) {
   const size_t f = sizeof(float) * (size_t) batch;
   const int64_t T1 = 4 * T, T2 = 16 * T, L = T2 + 1;

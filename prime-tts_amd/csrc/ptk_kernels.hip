@@ -877,6 +877,8 @@ extern "C" int ptk_leaky(const float *a, float *y, int64_t n, float alpha, void 
 // One workgroup produces TAIL_OUT consecutive samples; it recomputes the ~TAIL_OUT/16 + 5 frames
 // per band it needs (in LDS), so the whole tail is a single pass over p with no intermediates.
 #define TAIL_OUT 256
+// phase 4 maps thread t of a block to output o0 + t: one output per thread, the whole block
+static_assert(TAIL_OUT == 256, "tail_kernel runs 256 threads, one per output sample");
 #define TAIL_NY (TAIL_OUT / 4 + 18)
 #define TAIL_NT (TAIL_NY / 4 + 6)
 

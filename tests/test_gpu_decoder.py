@@ -146,6 +146,24 @@ def test_config4_decoder_T226_vs_oracle(env):
     assert np_ref.sndr(wav, ref) >= 60.0
 
 
+@pytest.mark.parametrize("L,batch", [(2, 1), (37, 2), (3617, 1)])
+def test_tail_alone_vs_oracle(env, L, batch):
+    """ptd_tail (the fused iSTFT + PQMF kernel) on random conv_post outputs against the oracle's
+    tail, per batch item: max |err| <= 1e-4 x RMS (exp / sin / cos on the device against libm)."""
+    ctx, model, ws, bs = env
+    say(f"tail alone L={L} batch={batch}")
+    rng = np.random.default_rng(L + batch)
+    p = (0.7 * rng.standard_normal((batch, 72, L))).astype(np.float32)
+    dp = dev_of(ctx, p)
+    dw = pkg.DevBuf(batch * 16 * (L - 1))
+    assert ctx.lib.ptd_tail(ctx.ptr, model.ptr, dp.ptr, L, batch, dw.ptr) == 0
+    got = dw.download(ctx).reshape(batch, 16 * (L - 1))
+    for i in range(batch):
+        ref = ol.tail(p[i], ws[40], bs[40])
+        assert relerr(got[i], ref) < 1e-4
+    dp.free(); dw.free()
+
+
 def test_decoder_final_conv_is_an_input():
     """The final PQMF synthesis conv (layer 40) comes from the caller's weights: a random filter
     with a bias gives the oracle's waveform, not the model constant's."""
