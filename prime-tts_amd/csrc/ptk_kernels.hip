@@ -11,6 +11,8 @@
 // applied on the accumulator values right before the single store.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include <type_traits>
 
 #include <stdarg.h>
@@ -44,17 +46,24 @@ static void set_err(const char *fmt, ...) {
 extern "C" const char *ptk_last_error(void) { return g_err; }
 
 // ------------------------------------------------------------------------------ runtime wrappers
+// Device 0 for the calling thread.  The device count is queried once per process; the current
+// device is per-thread HIP state, so every thread that creates a context selects it itself (the
+// reference brings contexts up from one thread per stream, concurrently).
 extern "C" int ptk_init(void) {
-  static int done = 0;
-  if (done) return 0;
-  int n = 0;
-  HCHK(hipGetDeviceCount(&n));
-  if (n < 1) {
+  static std::once_flag once;
+  static hipError_t count_err = hipSuccess;
+  static int ndev = 0;
+  std::call_once(once, [] { count_err = hipGetDeviceCount(&ndev); });
+  HCHK(count_err);
+  if (ndev < 1) {
     set_err("no HIP device");
     return -1;
   }
-  HCHK(hipSetDevice(0));
-  done = 1;
+  thread_local bool selected = false;
+  if (!selected) {
+    HCHK(hipSetDevice(0));
+    selected = true;
+  }
   return 0;
 }
 extern "C" int ptk_stream_create(void **s) {

@@ -304,3 +304,41 @@ def test_device_residency(ctx):
     p = lib.pt_v21_dev_alloc(ctx.ptr, 32 << 20)
     assert p == da
     lib.pt_v21_dev_free(ctx.ptr, p)
+
+
+def test_contexts_brought_up_concurrently():
+    """Eight contexts initialised at once from eight threads (the reference brings one up per
+    stream thread, concurrently: pt_v21_host.c:1149-1175, main_v21_par.c:63-73); each runs a conv
+    on its own stream that matches a single-threaded one bit for bit."""
+    import threading
+    say("8 contexts from 8 threads")
+    rng = np.random.default_rng(17)
+    x = rng.standard_normal((1, 64, 120)).astype(np.float32)
+    W = (rng.standard_normal((48, 64, 5)) / 18).astype(np.float32)
+    wp = synth.pack_conv(W)
+    b = rng.standard_normal(48).astype(np.float32)
+    base = pkg.Ctx(arena_mb=64)
+    want = gpu_conv(base, x, wp, b, 48, 5, 1, 2, 1)
+    ctxs, outs, errs = [None] * 8, [None] * 8, []
+    start = threading.Barrier(8)
+
+    def work(i):
+        try:
+            start.wait()
+            ctxs[i] = pkg.Ctx(arena_mb=64)
+            outs[i] = gpu_conv(ctxs[i], x, wp, b, 48, 5, 1, 2, 1)
+        except Exception as e:   # noqa: BLE001 - reported below
+            errs.append(repr(e))
+
+    ts = [threading.Thread(target=work, args=(i,)) for i in range(8)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    for c in ctxs:
+        if c is not None:
+            c.close()
+    base.close()
+    assert not errs, errs
+    for o in outs:
+        assert np.array_equal(o, want)
