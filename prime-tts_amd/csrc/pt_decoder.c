@@ -8,12 +8,14 @@
  *            residual and, for depths 0 and 1, also writes the LeakyReLU'd copy the next depth's
  *            c1 reads)  -> 6 launches, three branch outputs left in HBM.  ups.0 / ups.1 write
  *            their output and its LeakyReLU'd copy the same way.
- *   ups.1 convT 256->128: input staged as leaky(((b0 + b1) + b2) / 3, 0.1)
+ *   ups.1 convT 256->128 over leaky(((b0 + b1) + b2) / 3, 0.1), formed once by one elementwise
+ *            pass (cheaper than re-forming it in each of ups.1's 16 row blocks' staging)
  *   MRF-128 as above
- *   conv_post 128->72 K7: input staged as leaky((...)/3, 0.01) through the (1, 0) reflection pad
+ *   conv_post 128->72 K7 over leaky((...)/3, 0.01), formed the same way, through the (1, 0)
+ *            reflection pad
  *   tail: one kernel for exp/sin/cos -> irfft basis -> Hann -> OLA / window-sum -> [8:-8] ->
  *         PQMF x4 zero-insert -> 63-tap FIR
- * 17 launches per request, no host round trip.  The weights are uploaded once into one slab
+ * 19 launches per request, no host round trip.  The weights are uploaded once into one slab
  * owned by the model and shared by every context; each context brings its own stream + arena. */
 #define _GNU_SOURCE
 #include <math.h>
@@ -287,7 +289,7 @@ size_t ptd_decode_arena_bytes(int64_t T, int batch) {
   s += al256(f * 512 * T) + 2 * al256(f * 256 * T1) + 3 * al256(f * 256 * T1);   /* h, x0, x0L, o[] */
   size_t mrf0 = 9 * al256(f * 256 * T1);
   size_t late = 2 * al256(f * 128 * T2) + 3 * al256(f * 128 * T2) + 9 * al256(f * 128 * T2) +
-                al256(f * 72 * L);
+                al256(f * 72 * L) + al256(f * 256 * T1) + al256(f * 128 * T2);
   return s + (mrf0 > late ? mrf0 : late) + 4096;
 }
 
@@ -329,12 +331,10 @@ static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t ld
                   ptdi_arena_alloc(c, f * 128 * T2)};
   if (!x1 || !x1L || !o1[0] || !o1[1] || !o1[2]) goto oom;
   /* ups.1 over leaky(avg(branches), 0.1) */
-  ptdi_convT_desc(&d, o0[0], T1, 256 * T1, T1, 256, m->wr[20], m->b[20], 128, 4, 6, 16, x1, T2,
+  float *av0 = ptdi_arena_alloc(c, f * 256 * T1);
+  if (!av0 || ptk_avg3_leaky(o0[0], o0[1], o0[2], av0, (int64_t) batch * 256 * T1, 0.1f, c->g_stream)) goto fail;
+  ptdi_convT_desc(&d, av0, T1, 256 * T1, T1, 256, m->wr[20], m->b[20], 128, 4, 6, 16, x1, T2,
                   128 * T2, batch);
-  d.x1 = o0[1];
-  d.x2 = o0[2];
-  d.in_op = PTK_IN_AVG3_LEAKY;
-  d.in_a = 0.1f;
   d.y2 = x1L;
   d.a2 = 0.1f;
   if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
@@ -344,12 +344,10 @@ static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t ld
   float *p = ptdi_arena_alloc(c, f * 72 * L);
   if (!p) goto oom;
   /* conv_post over reflect_pad(1,0)(leaky(avg(branches), 0.01)) */
-  ptdi_conv_desc(&d, o1[0], T2, 128 * T2, L, 128, m->wr[39], m->b[39], 72, 7, 1, 1, 3, 72, p, L,
+  float *av1 = ptdi_arena_alloc(c, f * 128 * T2);
+  if (!av1 || ptk_avg3_leaky(o1[0], o1[1], o1[2], av1, (int64_t) batch * 128 * T2, 0.01f, c->g_stream)) goto fail;
+  ptdi_conv_desc(&d, av1, T2, 128 * T2, L, 128, m->wr[39], m->b[39], 72, 7, 1, 1, 3, 72, p, L,
                  72 * L, L, batch);
-  d.x1 = o1[1];
-  d.x2 = o1[2];
-  d.in_op = PTK_IN_AVG3_LEAKY;
-  d.in_a = 0.01f;
   d.reflect_l1 = 1;
   if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
   if (ptk_tail_batched(p, L, 72 * L, L, wav, bsw, batch, m->consts, emit, c->g_stream)) goto fail;

@@ -49,7 +49,7 @@ int ptk_device_sync(void);
  * c outside [0, lim) reads 0 (in-kernel zero padding and the convT tail flush).
  * Output for row m = r*C4 + co and column q goes to  y[b*bsy + co*ldy + (q*ys + r - ypad)]
  * when that index is in [0, Lout) (conv: C4 = M, ys = 1, ypad = 0). */
-enum { PTK_IN_PLAIN = 0, PTK_IN_LEAKY = 1, PTK_IN_AVG3_LEAKY = 2 };
+enum { PTK_IN_PLAIN = 0, PTK_IN_LEAKY = 1 };
 enum {
   PTK_EPI_NONE = 0,
   PTK_EPI_LEAKY = 1,   /* v >= 0 ? v : a*v                        (reference op code 1) */
@@ -71,7 +71,7 @@ typedef struct {
 
 typedef struct {
   /* input */
-  const float *x, *x1, *x2;   /* x1, x2 only for PTK_IN_AVG3_LEAKY */
+  const float *x;
   int64_t ldx, bsx;           /* row stride, batch stride (elements) */
   int64_t lim;                /* valid virtual input columns [0, lim) */
   int cin;

@@ -252,22 +252,12 @@ __device__ __forceinline__ float epi_apply(float v, const ptk_epi &e, int b, int
   }
 }
 
-// input transform applied as a window element is staged (the reference's separate LeakyReLU /
-// Add / Div nodes in front of a conv, fused): IN is a PTK_IN_* code
+// input transform applied as a window element is staged (the reference's separate LeakyReLU node
+// in front of a conv, fused): IN is a PTK_IN_* code.
 // LeakyReLU as max(v, a*v): identical to (v >= 0 ? v : a*v) for 0 <= a <= 1 (signed zeros
 // included), which the launcher enforces, in two instructions instead of three.
-// The division by 3 uses q = x * r, r = RN(1/3), corrected once with the exact residual
-// fma(-q, 3, x): checked exhaustively against IEEE x / 3 over every finite float, it differs only
-// for x = -0 (gives +0), which no conv output can tell apart.  Three instructions instead of the
-// ten of a general division.
 template <int IN>
-__device__ __forceinline__ float in_xform(float v, float v1, float v2, float a) {
-  if constexpr (IN == PTK_IN_AVG3_LEAKY) {
-    constexpr float r3 = 1.0f / 3.0f;
-    const float s = (v + v1) + v2;
-    const float q = s * r3;
-    v = __builtin_fmaf(__builtin_fmaf(-q, 3.0f, s), r3, q);
-  }
+__device__ __forceinline__ float in_xform(float v, float a) {
   if constexpr (IN != PTK_IN_PLAIN) v = fmaxf(v, a * v);
   return v;
 }
@@ -320,7 +310,6 @@ template <int KT, int NB, int IN>
 __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   extern __shared__ float smem[];
   constexpr int NJ = WinGeo<NB>::NJ, XWMAX = WinGeo<NB>::XWMAX;
-  constexpr int NX = IN == PTK_IN_AVG3_LEAKY ? 3 : 1;
   int bid = blockIdx.x;
   int p = 0;
 #pragma unroll
@@ -367,11 +356,6 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   const unsigned nrec = (unsigned) cin * ldx4;
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
       (void *) (d.x + xoff), (short) 0, (int) nrec, PTK_BUF_WORD3);
-  __amdgpu_buffer_rsrc_t rx1 = rx, rx2 = rx;
-  if constexpr (NX == 3) {
-    rx1 = __builtin_amdgcn_make_buffer_rsrc((void *) (d.x1 + xoff), (short) 0, (int) nrec, PTK_BUF_WORD3);
-    rx2 = __builtin_amdgcn_make_buffer_rsrc((void *) (d.x2 + xoff), (short) 0, (int) nrec, PTK_BUF_WORD3);
-  }
   unsigned voff[NJ];
 #pragma unroll
   for (int jj = 0; jj < NJ; jj++) {
@@ -384,18 +368,14 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
 
   // Staging is split so that all global loads of a chunk are in flight together: the load phase
   // only issues loads, the store phase (one chunk later) transforms and writes LDS.
-  float pf[NX][CONV_CK][NJ];
+  float pf[CONV_CK][NJ];
   auto load_chunk = [&](int c0) {
 #pragma unroll
     for (int r = 0; r < CONV_CK; r++) {
       const unsigned rowo = c0 + r < cin ? (unsigned) (c0 + r) * ldx4 : 0u;
 #pragma unroll
       for (int jj = 0; jj < NJ; jj++) {
-        pf[0][r][jj] = buf_load(rx, voff[jj], rowo);
-        if constexpr (NX == 3) {
-          pf[1][r][jj] = buf_load(rx1, voff[jj], rowo);
-          pf[2][r][jj] = buf_load(rx2, voff[jj], rowo);
-        }
+        pf[r][jj] = buf_load(rx, voff[jj], rowo);
       }
     }
   };
@@ -406,8 +386,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
       float v[CONV_CK];
 #pragma unroll
       for (int r = 0; r < CONV_CK; r++) {
-        if constexpr (NX == 3) v[r] = in_xform<IN>(pf[0][r][jj], pf[1][r][jj], pf[2][r][jj], in_a);
-        else v[r] = in_xform<IN>(pf[0][r][jj], 0.0f, 0.0f, in_a);
+        v[r] = in_xform<IN>(pf[r][jj], in_a);
       }
       if (nlive < CONV_CK) {
 #pragma unroll
@@ -617,7 +596,6 @@ template <int NB>
 static void launch_conv_in(int in_op, int kmax, const ConvGroup &g, int nblk, size_t lds,
                            hipStream_t s) {
   if (in_op == PTK_IN_LEAKY) launch_conv_k<NB, PTK_IN_LEAKY>(kmax, g, nblk, lds, s);
-  else if (in_op == PTK_IN_AVG3_LEAKY) launch_conv_k<NB, PTK_IN_AVG3_LEAKY>(kmax, g, nblk, lds, s);
   else launch_conv_k<NB, PTK_IN_PLAIN>(kmax, g, nblk, lds, s);
 }
 
@@ -655,8 +633,7 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
       return -1;
     }
     if (in_op < 0) in_op = d->in_op;
-    if (d->in_op != in_op || d->in_op < PTK_IN_PLAIN || d->in_op > PTK_IN_AVG3_LEAKY ||
-        (d->in_op == PTK_IN_AVG3_LEAKY && (!d->x1 || !d->x2))) {
+    if (d->in_op != in_op || d->in_op < PTK_IN_PLAIN || d->in_op > PTK_IN_LEAKY) {
       set_err("ptk_conv_launch: grouped problems need one valid input transform");
       return -1;
     }
