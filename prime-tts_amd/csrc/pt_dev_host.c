@@ -414,6 +414,11 @@ static void add_ref_epi(ptk_conv_desc *d, int op, float a) {
 }
 
 /* ================================================================== pt_v21_conv */
+static int fail_oom(const char *what) {
+  PT_LOG("%s: host allocation failed", what);
+  return -1;
+}
+
 static int fail_cpu(const char *what) {
   PT_LOG("%s on a context without the device and no host CPU path linked", what);
   return -1;
@@ -652,12 +657,20 @@ int pt_v21_matmul(pt_ctx *c, const float *A, int64_t m, int64_t k, int64_t lda, 
     PT_LOG("pt_v21_matmul: bad arguments");
     return -1;
   }
-  /* tight device copies: only the k (A), n (B, C) columns each row uses are moved, so no byte
+  /* Tight device copies.  Only the k (A) and n (B, C) columns of each row are moved, so no byte
    * outside the matrices is read, and C's padding columns (ldc > n) are left as they are, as the
-   * reference's CPU matmul leaves them (pt_v21_host.c:2635-2650) */
-  const size_t ab = (size_t) m * (k > 0 ? k : 1) * sizeof(float);
-  const size_t bb = (size_t) (k > 0 ? k : 1) * nn * sizeof(float);
-  const size_t cb = (size_t) m * nn * sizeof(float);
+   * reference's CPU matmul leaves them (pt_v21_host.c:2635-2650).  Each matrix goes in one
+   * contiguous copy; padded rows are packed / scattered on the host (a pageable 2-D copy moves
+   * row by row, tens of microseconds per row). */
+  const size_t f = sizeof(float);
+  const size_t ab = (size_t) m * (k > 0 ? k : 1) * f, bb = (size_t) (k > 0 ? k : 1) * nn * f;
+  const size_t cb = (size_t) m * nn * f;
+  float *hA = NULL, *hB = NULL, *hC = NULL;   /* host staging for padded rows */
+  if (k > 0 && lda != k && !(hA = malloc(ab))) return fail_oom("pt_v21_matmul");
+  if (k > 0 && ldb != nn && !(hB = malloc(bb))) { free(hA); return fail_oom("pt_v21_matmul"); }
+  if (ldc != nn && !(hC = malloc(cb))) { free(hA); free(hB); return fail_oom("pt_v21_matmul"); }
+  for (int64_t i = 0; hA && i < m; i++) memcpy(hA + i * k, A + i * lda, (size_t) k * f);
+  for (int64_t i = 0; hB && i < k; i++) memcpy(hB + i * nn, B + i * ldb, (size_t) nn * f);
   void *mark = ptdi_arena_mark(c);
   float *dA = ptdi_arena_alloc(c, ab), *dB = ptdi_arena_alloc(c, bb), *dC = ptdi_arena_alloc(c, cb);
   int own = 0;
@@ -666,23 +679,25 @@ int pt_v21_matmul(pt_ctx *c, const float *A, int64_t m, int64_t k, int64_t lda, 
     dA = dB = dC = NULL;
     if (ptk_malloc((void **) &dA, ab) || ptk_malloc((void **) &dB, bb) || ptk_malloc((void **) &dC, cb)) {
       ptk_free(dA); ptk_free(dB); ptk_free(dC);
+      free(hA); free(hB); free(hC);
       PT_LOG("pt_v21_matmul: allocation failed: %s", ptk_last_error());
       return -1;
     }
     own = 1;
   }
-  const size_t f = sizeof(float);
-  int r = (k > 0 && (ptk_h2d_2d_async(dA, (size_t) k * f, A, (size_t) lda * f, (size_t) k * f, (size_t) m, c->g_stream) ||
-                     ptk_h2d_2d_async(dB, (size_t) nn * f, B, (size_t) ldb * f, (size_t) nn * f, (size_t) k, c->g_stream))) ||
+  int r = (k > 0 && (ptk_h2d_async(dA, hA ? hA : A, (size_t) m * k * f, c->g_stream) ||
+                     ptk_h2d_async(dB, hB ? hB : B, (size_t) k * nn * f, c->g_stream))) ||
           ptk_matmul(dA, m, k, k, dB, nn, nn, dC, nn, c->g_stream) || ptdi_wait(c) ||
-          ptk_d2h_2d_async(C, (size_t) ldc * f, dC, (size_t) nn * f, (size_t) nn * f, (size_t) m, c->g_stream) ||
-          ptk_stream_sync(c->g_stream);
+          ptk_d2h_async(hC ? hC : C, dC, cb, c->g_stream) || ptk_stream_sync(c->g_stream);
+  if (!r && hC)
+    for (int64_t i = 0; i < m; i++) memcpy(C + i * ldc, hC + i * nn, (size_t) nn * f);
   if (r) PT_LOG("pt_v21_matmul failed: %s", ptk_last_error());
   if (own) {
     ptk_free(dA); ptk_free(dB); ptk_free(dC);
   } else {
     ptdi_arena_release(c, mark);
   }
+  free(hA); free(hB); free(hC);
   return r ? -1 : 0;
 }
 
