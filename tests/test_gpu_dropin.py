@@ -4,7 +4,9 @@ runs a synthetic full PrimeTTS v2.1 model twice: as the reference's CPU build, a
 -DPT_V21_CUDA and linked against libptconv_hip.so, so that every conv, convT and matmul of the
 graph goes through this library's C ABI on the MI355X.  The device build must reproduce the CPU
 build's waveform: the driver's own parity gate (SNDR >= 60 dB, main_v21.c) and the same check
-here.  Skipped where oracle/_ref was not built (the reference tree is absent)."""
+here.  The reference's multi-stream driver (main_v21_par.c) then runs eight concurrent streams,
+each bringing up its own context on its own thread against one shared weight pool, under the
+same gate.  Skipped where oracle/_ref was not built (the reference tree is absent)."""
 from __future__ import annotations
 
 import re
@@ -20,7 +22,7 @@ import np_ref
 from conftest import ROOT
 
 REF = ROOT / "oracle" / "_ref"
-CPU_BIN, DEV_BIN = REF / "pt_v21_cpu", REF / "pt_v21_mi355x"
+CPU_BIN, DEV_BIN, PAR_BIN = REF / "pt_v21_cpu", REF / "pt_v21_mi355x", REF / "pt_v21_par_mi355x"
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not (CPU_BIN.exists() and DEV_BIN.exists()),
                                  reason="oracle/_ref driver builds absent (reference tree not present)")]
@@ -57,3 +59,10 @@ def test_reference_driver_through_the_library(tmp_path):
     m = re.search(r"conv=(\d+) convT=(\d+) matmul=(\d+)", r.stdout)
     assert m and tuple(int(v) for v in m.groups()) == (124, 5, 50), r.stdout
     assert "pt_v21 hip: context ready" in r.stderr
+    if PAR_BIN.exists():
+        say("reference multi-stream driver, 8 streams")
+        rp = _run([PAR_BIN, "--container", tmp_path / "model.ptk", "--case", case, "--parallel", 8], 300)
+        # the driver's own gate: every stream >= 60 dB against the CPU build's waveform
+        assert rp.returncode == 0, rp.stdout + rp.stderr
+        sndrs = [float(v) for v in re.findall(r"stream \d+: L=\d+ .*?SNDR=([0-9.]+) dB", rp.stdout)]
+        assert len(sndrs) == 8 and min(sndrs) >= 60.0, rp.stdout
