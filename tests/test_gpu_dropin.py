@@ -32,25 +32,47 @@ def say(msg):
     print(f"[gpu dropin] {msg}", file=sys.stderr, flush=True)
 
 
-def _run(cmd, timeout):
-    r = subprocess.run([str(x) for x in cmd], capture_output=True, text=True, timeout=timeout)
+def _run(cmd, timeout, env=None):
+    import os
+    full_env = dict(os.environ, **(env or {}))
+    r = subprocess.run([str(x) for x in cmd], capture_output=True, text=True, timeout=timeout,
+                       env=full_env)
     for line in (r.stdout + r.stderr).splitlines()[-8:]:
         say(line)
     return r
 
 
-def test_reference_driver_through_the_library(tmp_path):
+@pytest.fixture(scope="module")
+def model(tmp_path_factory):
+    """A synthetic full model, a 40-token case, and the reference CPU build's waveform for it
+    (stored as the case's wav.npy, which the drivers compare against)."""
+    d = tmp_path_factory.mktemp("dropin")
     say("synthetic full model + 40-token case")
-    fm.write_container(tmp_path / "model.ptk", seed=0)
-    case = tmp_path / "case"
+    fm.write_container(d / "model.ptk", seed=0)
+    case = d / "case"
     fm.write_case(case, n_tokens=40, seed=0)
-    cpu_wav, dev_wav = tmp_path / "cpu.npy", tmp_path / "dev.npy"
+    cpu_wav = d / "cpu.npy"
     say("reference CPU build")
-    _run([CPU_BIN, "--cpu", "--container", tmp_path / "model.ptk", "--case", case, "--out", cpu_wav], 600)
+    _run([CPU_BIN, "--cpu", "--container", d / "model.ptk", "--case", case, "--out", cpu_wav], 600)
     assert cpu_wav.exists()
     shutil.copy(cpu_wav, case / "wav.npy")
-    say("reference driver linked against libptconv_hip.so")
-    r = _run([DEV_BIN, "--container", tmp_path / "model.ptk", "--case", case, "--out", dev_wav], 300)
+    return d, case, cpu_wav
+
+
+# the host's own switches (pt_v21_host.c): defaults (epilogue fusion and conv chains on), device
+# residency for the residual adds and activations on (PT_V21_DEVADD, :2364-2543), and fusion and
+# chaining off (every conv a plain call, every Add / LeakyRelu a host op)
+HOST_MODES = {"default": {}, "devadd": {"PT_V21_DEVADD": "1"},
+              "unfused": {"PT_V21_FUSE": "0", "PT_V21_CHAIN": "0"}}
+
+
+@pytest.mark.parametrize("mode", list(HOST_MODES))
+def test_reference_driver_through_the_library(model, tmp_path, mode):
+    d, case, cpu_wav = model
+    dev_wav = tmp_path / "dev.npy"
+    say(f"reference driver linked against libptconv_hip.so, host mode {mode}")
+    r = _run([DEV_BIN, "--container", d / "model.ptk", "--case", case, "--out", dev_wav], 300,
+             HOST_MODES[mode])
     assert r.returncode == 0, "the driver's own gate (SNDR >= 60 dB against the CPU build) failed"
     a, b = np.load(dev_wav).ravel(), np.load(cpu_wav).ravel()
     assert a.shape == b.shape and a.size > 10000
@@ -59,10 +81,14 @@ def test_reference_driver_through_the_library(tmp_path):
     m = re.search(r"conv=(\d+) convT=(\d+) matmul=(\d+)", r.stdout)
     assert m and tuple(int(v) for v in m.groups()) == (124, 5, 50), r.stdout
     assert "pt_v21 hip: context ready" in r.stderr
-    if PAR_BIN.exists():
-        say("reference multi-stream driver, 8 streams")
-        rp = _run([PAR_BIN, "--container", tmp_path / "model.ptk", "--case", case, "--parallel", 8], 300)
-        # the driver's own gate: every stream >= 60 dB against the CPU build's waveform
-        assert rp.returncode == 0, rp.stdout + rp.stderr
-        sndrs = [float(v) for v in re.findall(r"stream \d+: L=\d+ .*?SNDR=([0-9.]+) dB", rp.stdout)]
-        assert len(sndrs) == 8 and min(sndrs) >= 60.0, rp.stdout
+
+
+@pytest.mark.skipif(not PAR_BIN.exists(), reason="oracle/_ref/pt_v21_par_mi355x not built")
+def test_reference_multistream_driver(model):
+    d, case, _ = model
+    say("reference multi-stream driver, 8 streams")
+    rp = _run([PAR_BIN, "--container", d / "model.ptk", "--case", case, "--parallel", 8], 300)
+    # the driver's own gate: every stream >= 60 dB against the CPU build's waveform
+    assert rp.returncode == 0, rp.stdout + rp.stderr
+    sndrs = [float(v) for v in re.findall(r"stream \d+: L=\d+ .*?SNDR=([0-9.]+) dB", rp.stdout)]
+    assert len(sndrs) == 8 and min(sndrs) >= 60.0, rp.stdout
