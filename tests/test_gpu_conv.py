@@ -342,3 +342,76 @@ def test_contexts_brought_up_concurrently():
     assert not errs, errs
     for o in outs:
         assert np.array_equal(o, want)
+
+
+def _random_conv_cases(n=48, seed=2024):
+    """Seeded random pt_v21_conv calls: odd channel counts around the 4/8/32 tile edges, lengths
+    that leave partial column tiles, strides, dilations, both row layouts, padded output rows,
+    batch, and every pair of the reference's epilogue codes."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n:
+        B = int(rng.integers(1, 4))
+        cin = int(rng.choice([2, 3, 7, 8, 9, 16, 31, 33, 64, 96, 130, 192, 257]))
+        cout = int(rng.choice([1, 2, 4, 5, 15, 16, 17, 31, 32, 33, 64, 72, 100, 129, 256]))
+        K = int(rng.integers(1, 12))
+        dil = int(rng.integers(1, 6)) if K > 1 else 1
+        stride = int(rng.choice([1, 1, 1, 2, 3]))
+        pad = int(rng.integers(0, (K - 1) * dil // 2 + 2))
+        T = int(rng.integers(1, 300))
+        Tout = (T + 2 * pad - (K - 1) * dil - 1) // stride + 1
+        if Tout < 1 or B * cin * cout * K * Tout > 3e7:
+            continue
+        e0, e1 = (int(v) for v in rng.integers(0, 5, 2))
+        cases.append((B, cin, cout, T, K, stride, pad, dil, e0, e1, bool(rng.integers(0, 2)),
+                      int(rng.choice([0, 0, 5]))))
+    return cases
+
+
+@pytest.mark.parametrize("cfg", _random_conv_cases(), ids=lambda c: "-".join(str(int(v)) for v in c))
+def test_conv_random_vs_oracle(ctx, cfg):
+    B, cin, cout, T, K, s, pad, d, e0, e1, padded, ldy_extra = cfg
+    say(f"conv random {cfg}")
+    rng = np.random.default_rng(abs(hash(cfg)) % (1 << 32))
+    x = rng.standard_normal((B, cin, T)).astype(np.float32)
+    W = (rng.standard_normal((cout, cin, K)) / np.sqrt(cin * K)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(cout)).astype(np.float32) if rng.integers(0, 4) else None
+    wp = synth.pack_conv(W)
+    ref = ol.conv(x, wp, b, cout, K, s, pad, d, e0, e1, 0.1, 0.5)
+    y = gpu_conv(ctx, x, wp, b, cout, K, s, pad, d, e0, e1, 0.1, 0.5, padded=padded,
+                 ldy_extra=ldy_extra)
+    assert y.shape == ref.shape
+    assert relerr(y, ref) < TOL
+
+
+def _random_convT_cases(n=24, seed=7):
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n:
+        B = int(rng.integers(1, 4))
+        cin = int(rng.choice([1, 2, 5, 16, 33, 64, 130, 256]))
+        cout = int(rng.choice([1, 3, 4, 16, 17, 36, 64, 128]))
+        K = int(rng.integers(1, 18))
+        s = int(rng.integers(1, 6))
+        pad = int(rng.integers(0, K))
+        tin = int(rng.integers(1, 200))
+        Lout = (tin - 1) * s - 2 * pad + K
+        if Lout < 1 or B * cin * cout * K * tin > 3e7:
+            continue
+        cases.append((B, cin, cout, tin, K, s, pad))
+    return cases
+
+
+@pytest.mark.parametrize("cfg", _random_convT_cases(), ids=lambda c: "-".join(str(v) for v in c))
+def test_convT_random_vs_oracle(ctx, cfg):
+    B, cin, cout, tin, K, s, pad = cfg
+    say(f"convT random {cfg}")
+    rng = np.random.default_rng(sum(cfg) * 7919)
+    x = rng.standard_normal((B, cin, tin)).astype(np.float32)
+    W = (rng.standard_normal((cin, cout, K)) / np.sqrt(max(cin * K / s, 1.0))).astype(np.float32)
+    b = (0.1 * rng.standard_normal(cout)).astype(np.float32)
+    wp = synth.pack_convtranspose(W, s)
+    ref = ol.convT(x, wp, b, cout, K, s, pad)
+    y = gpu_convT(ctx, x, wp, b, cout, K, s, pad)
+    assert y.shape == ref.shape
+    assert relerr(y, ref) < TOL
