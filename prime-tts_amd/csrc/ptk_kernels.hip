@@ -15,6 +15,7 @@
 
 #include <type_traits>
 
+#include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -543,21 +544,47 @@ static int env_knob(const char *name) {
   return e ? atoi(e) : 0;
 }
 
-// channel split: the smallest S in {1, 2, 4} whose grid still gives every SIMD about two waves,
-// else 4 (PTK_CONV_SPLIT overrides)
+// Channel split S in {1, 2, 4} (PTK_CONV_SPLIT overrides).  All waves of a launch usually fit on
+// the chip at once, so a launch lasts as long as its busiest SIMD: with W waves over the 1024
+// SIMDs (256 CUs x 4) that SIMD holds ceil(W / 1024) of them while the mean is W / 1024.  Fewer
+// than ~3 waves per SIMD also leave MFMA latency exposed (a lone wave keeps its SIMD's matrix
+// pipe ~60 % busy), and each split step costs its LDS reduction and a share of the edges.  The
+// model below, fitted to decoder shapes measured on MI355X (batch 1 and 22, C 128 / 256, K 3-11),
+// picks the S with the best predicted MFMA occupancy:
+//   eff(S) = [mean / max waves per SIMD] x [latency hiding at the mean] x [split cost]
+// evaluated on ONE batch item's grid.  S fixes the order in which a block's partial sums are
+// added, so choosing it without the batch size makes a batched item's result bit-identical to
+// the same item decoded alone (and it measured faster at batch 8 than a batch-aware choice).
+static const double kSimds = 1024.0;
+static double split_eff(long long waves, int S) {
+  const double m = (double) waves / kSimds;
+  // past residency the extra waves run as one more wave on the SIMDs they land on
+  const double busiest = ceil(m);
+  const double balance = m / (busiest > 0.0 ? busiest : 1.0);
+  const double mh = m < 4.0 ? m : 4.0;
+  const double hide = mh >= 2.75 ? 1.0 : 0.45 + 0.2 * mh;
+  const double cost = S == 1 ? 1.0 : (S == 2 ? 0.97 : 0.90);
+  return balance * hide * cost;
+}
 static int choose_split(const ptk_conv_desc *const *ds, int n, int nb) {
   const int env = env_knob("PTK_CONV_SPLIT");
   if (env == 1 || env == 2 || env == 4) return env;
-  for (int S = 1; S < 4; S *= 2) {
+  int best = 4;
+  double best_eff = -1.0;
+  for (int S = 1; S <= 4; S *= 2) {
     const int G = 4 / S;
     long long waves = 0;
     for (int i = 0; i < n; i++) {
       const ptk_conv_desc *d = ds[i];
-      waves += 4LL * ((d->M + 31) / 32) * ((d->nq + 32LL * nb * G - 1) / (32LL * nb * G)) * d->batch;
+      waves += 4LL * ((d->M + 31) / 32) * ((d->nq + 32LL * nb * G - 1) / (32LL * nb * G));
     }
-    if (waves >= 2048) return S;
+    const double e = split_eff(waves, S);
+    if (e > best_eff + 1e-9) {
+      best_eff = e;
+      best = S;
+    }
   }
-  return 4;
+  return best;
 }
 
 // column blocks per wave: 1.  Two blocks halve the weight loads per MFMA but double the window

@@ -182,18 +182,19 @@ def test_decoder_final_conv_is_an_input():
     assert np_ref.sndr(wav, ref) >= 60.0
 
 
-def test_batched_decode_matches_single(env):
-    """batch > 1 (used by the windowed path) equals per-item decodes bit for bit."""
+@pytest.mark.parametrize("T,batch", [(24, 3), (226, 8)])
+def test_batched_decode_matches_single(env, T, batch):
+    """batch > 1 (used by the windowed path) equals per-item decodes bit for bit: the conv tiling,
+    the channel split included, is chosen from one item's shape, never from the batch size."""
     ctx, model, ws, bs = env
-    say("batched decode")
-    T = 24
-    zs = [synth.latent(T, 500 + i) for i in range(3)]
+    say(f"batched decode T={T} batch={batch}")
+    zs = [synth.latent(T, 500 + i) for i in range(batch)]
     singles = [_decode(ctx, model, z) for z in zs]
     dz = dev_of(ctx, np.stack(zs))
-    dw = pkg.DevBuf(3 * 256 * T)
-    assert ctx.lib.ptd_decode(ctx.ptr, model.ptr, dz.ptr, T, 3, dw.ptr) == 0
-    wb = dw.download(ctx).reshape(3, 256 * T)
-    for i in range(3):
+    dw = pkg.DevBuf(batch * 256 * T)
+    assert ctx.lib.ptd_decode(ctx.ptr, model.ptr, dz.ptr, T, batch, dw.ptr) == 0
+    wb = dw.download(ctx).reshape(batch, 256 * T)
+    for i in range(batch):
         assert np.array_equal(wb[i], singles[i])
     dz.free(); dw.free()
 
