@@ -184,9 +184,8 @@ static float *pack_convT_c(const float *W, int cin, int cout, int K, int s) {
  * values it reproduces), the window-sum kernel is its square (trace :3617 onnx::ConvTranspose_5159).
  * irfft basis for n_fft 16 (trace :3607-3615): row k of the cos basis is w_k cos(2 pi k n/16)/16 and
  * of the sin basis -w_k sin(2 pi k n / 16)/16, w = [1, 2, ..., 2, 1] (k = 0..8).
- * PQMF: /dec/Constant_134 is a model constant (only 8 of 252 values are visible in the trace), so
- * the synthetic decoder fixes its own: the Kaiser-windowed sinc prototype with 62 taps, cutoff
- * 0.142, beta 9, cosine-modulated for 4 bands with phase -(-1)^k pi/4, gain 2. */
+ * The PQMF synthesis filter is not a closed form: it is the model constant /dec/Constant_134, the
+ * weight of the final conv, and comes in as decoder layer 40 (orc_tail's wfir / bfir). */
 void orc_dec_constants(float *hann16, float *basis_c, float *basis_s) {
   const double pi = 3.14159265358979323846;
   if (hann16)

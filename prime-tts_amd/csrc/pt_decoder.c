@@ -56,7 +56,7 @@ static layer_geo dec_geo(int i) {
 
 struct ptd_model {
   void *slab;                      /* relaid weights, biases, tail constants */
-  const float *wr[PTD_DEC_NLAYER]; /* MFMA layout [Mp/32][K][cinp][32] */
+  const float *wr[PTD_DEC_NLAYER]; /* MFMA layout [Mp/32][K][cinp/8][64][4] */
   const float *b[PTD_DEC_NLAYER];
   const float *consts;             /* the tail's table: hann, basis_c, basis_s, final conv */
   layer_geo g[PTD_DEC_NLAYER];

@@ -78,7 +78,7 @@ typedef struct {
   int in_op;
   float in_a;
   int reflect_l1;             /* virtual column 0 reads physical column 1, column c>0 reads c-1 */
-  /* weights: relaid [Mp/32][K][cinp][32] (see ptk_relayout) */
+  /* weights: relaid [Mp/32][K][cinp/8][64][4] (see ptk_relayout) */
   const float *w;
   int cinp;
   const float *bias;
@@ -101,7 +101,7 @@ typedef struct {
 } ptk_conv_desc;
 
 /* Relayout packed conv/convT weights [M/4][K][cin][4] into the MFMA operand layout
- * [Mp/32][K][cinp][32] (Mp = M rounded up to 32, zero rows/channels in the padding).  Returns the
+ * [Mp/32][K][cinp/8][64 lanes][4] (Mp = M rounded up to 32, zero rows/channels in the padding).  Returns the
  * cinp the kernels expect for this cin (ptk_conv_cinp). */
 int ptk_conv_cinp(int cin);
 size_t ptk_relayout_floats(int M, int K, int cin);
