@@ -6,7 +6,8 @@ One step = BASELINE config 5, the largest single-GPU configuration: 8 independen
 long-form request of T = 1500 frames through 96-frame overlap-save windows with 16-frame context
 on a ninth context, all sharing one uploaded weight set.  Inputs are resident in HBM before the
 timed region; `value` is the step's audio seconds divided by its wall time.  Alongside: config 4
-(one request, T = 226) on one stream, configs 1-3 in TFLOP/s, the dominant kernel against the
+(one request, T = 226) on one stream, the long-form request window by window (time to first
+audio) and batched, configs 1-3 in TFLOP/s, the dominant kernel against the
 fp32-MFMA roofline (HIP events on the stream it runs on), and the reference's CPU conv path timed
 on this host on a bounded sample.
 
@@ -267,6 +268,40 @@ def main():
         b.free()
     log(f"configs: {cfg}")
 
+    # ---------------------------------------------------------------- streaming (config 5's
+    # long-form request on one stream): the first 96-frame window alone (time to first audio),
+    # every window one at a time as the reference's --stream driver issues them, and the batched
+    # windowed decode
+    T_long, WIN, CTX = 1500, 96, 16
+    zl = pkg.DevBuf.of(ctx, pkg.synth.latent(T_long, 900 + 8))
+    pcm, wl = pkg.DevBuf(HOP * WIN), pkg.DevBuf(HOP * T_long)
+    nout = C.c_int64()
+    starts = list(range(0, T_long, WIN - 2 * CTX))
+    starts = starts[:next(i for i, a in enumerate(starts) if a + WIN >= T_long) + 1]
+
+    def chunk(a):
+        if lib.ptd_decode_chunk(ctx.ptr, model.ptr, zl.ptr, T_long, a, WIN, pcm.ptr, C.byref(nout)) != 0:
+            raise RuntimeError("chunk decode failed")
+
+    def all_chunks():
+        for a in starts:
+            chunk(a)
+
+    def batched():
+        if lib.ptd_decode_windows(ctx.ptr, model.ptr, zl.ptr, T_long, WIN, CTX, wl.ptr) != 0:
+            raise RuntimeError("windowed decode failed")
+
+    for f in (all_chunks, batched):
+        f()
+    stream = {"frames": T_long, "win": WIN, "ctx": CTX, "windows": len(starts),
+              "first_chunk_ms": round(timer.time(lambda: chunk(0), 20), 4),
+              "chunked_total_ms": round(timer.time(all_chunks, 5), 4),
+              "batched_windows_ms": round(timer.time(batched, 10), 4)}
+    stream["audio_s"] = round(T_long * HOP / SR, 4)
+    for b in (zl, pcm, wl):
+        b.free()
+    log(f"streaming: {stream}")
+
     # ---------------------------------------------------------------- config 5: the timed step
     Ts = pkg.synth.request_lengths(5, 8)
     T_long = 1500
@@ -334,6 +369,7 @@ def main():
             "bound": "hbm", "peak_gbps": HBM_PEAK,
             "alg_bytes_per_request": tail_bytes(TAIL_L, 1), **tail,
         },
+        "streaming": stream,
         **cfg,
     }
     if not args.no_cpu_baseline:

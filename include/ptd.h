@@ -124,6 +124,15 @@ int ptd_decode_windows(pt_ctx *c, const ptd_model *m, const float *z, int64_t T,
                        float *wav);
 size_t ptd_windows_arena_bytes(int64_t T, int win, int ctx);
 
+/* One window of a sequence, for audio as it is decoded (replaces pt_v21_stream_chunk,
+ * pt_v21.h:194, pt_v21_host.c:2871-2902): a < 0 reads as 0, win < 1 as 1, and the window is
+ * clipped to [a, T); -1 if nothing is left.  pcm (device, >= 256*win floats) receives the whole
+ * window's waveform and *n its length (256 x the clipped width); the caller keeps the interior,
+ * as main_v21.c:344-362 does.  z [192][T] read in place; arena as ptd_decode_arena_bytes(win, 1).
+ * Asynchronous. */
+int ptd_decode_chunk(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int64_t a,
+                     int64_t win, float *pcm, int64_t *n);
+
 /* ---- concurrent serving (config 5; the reference's main_v21_par.c:59-158 model) ------------ *
  * nctx contexts (one stream + arena each, sharing the model's weights), each driven by its own
  * pthread.  ptd_serve_run hands request r to context r % nctx, runs all requests, waits for

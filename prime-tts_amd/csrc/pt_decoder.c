@@ -514,6 +514,22 @@ int ptd_decode_windows(pt_ctx *c, const ptd_model *m, const float *z, int64_t T,
   return rc;
 }
 
+/* One window at a time, for a caller that plays audio as it arrives (pt_v21_stream_chunk,
+ * pt_v21_host.c:2871-2902): the same clipping of [a, a + win) to the sequence, and the window's
+ * whole waveform (256 samples a frame) to pcm.  A batch-1 decode reading z in place. */
+int ptd_decode_chunk(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int64_t a,
+                     int64_t win, float *pcm, int64_t *n) {
+  if (n) *n = 0;
+  if (!c || !m || !z || !pcm || T < 1) return -1;
+  if (a < 0) a = 0;
+  if (win < 1) win = 1;
+  if (a + win > T) win = T - a;
+  if (win < 1) return -1;
+  if (decode_impl(c, m, z + a, T, 0, win, 1, pcm, 0, NULL, NULL)) return -1;
+  if (n) *n = win * 256;
+  return 0;
+}
+
 /* ------------------------------------------------------------------ concurrent serving */
 struct ptd_server {
   int n;

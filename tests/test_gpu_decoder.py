@@ -279,6 +279,69 @@ def test_config5_longform_windows_vs_full(env):
     dz.free(); dw.free()
 
 
+@pytest.mark.parametrize("T,win,cx", [(20, 32, 8), (57, 32, 8), (70, 32, 8), (300, 96, 16)])
+def test_stream_chunks_stitched_equal_windows(env, T, win, cx):
+    """ptd_decode_chunk window by window, stitched the way the reference's --stream driver does
+    (main_v21.c:341-362: step win - 2*ctx, keep [ctx, win_eff - ctx) frames of each window, the
+    first from 0 and the last to its end), equals the batched ptd_decode_windows bit for bit."""
+    ctx, model, ws, bs = env
+    say(f"stream chunks T={T} win={win} ctx={cx}")
+    lib = ctx.lib
+    z = synth.latent(T, 500 + T)
+    dz = dev_of(ctx, z)
+    dp = pkg.DevBuf(256 * win)
+    n = C.c_int64(0)
+    out = []
+    step = max(win - 2 * cx, 1)
+    a = 0
+    while True:
+        w = min(win, T - a)
+        first, last = a == 0, a + w >= T
+        assert lib.ptd_decode_chunk(ctx.ptr, model.ptr, dz.ptr, T, a, w, dp.ptr, C.byref(n)) == 0
+        assert n.value == 256 * w
+        pcm = dp.download(ctx)[:n.value]
+        lo = 0 if first else cx * 256
+        hi = n.value if last else min((w - cx) * 256, n.value)
+        if hi > lo:
+            out.append(pcm[lo:hi])
+        if last:
+            break
+        a += step
+    stitched = np.concatenate(out)
+    dw = pkg.DevBuf(256 * T)
+    assert lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, win, cx, dw.ptr) == 0
+    wav = dw.download(ctx)
+    assert stitched.shape == wav.shape
+    assert np.array_equal(stitched, wav), f"max diff {np.max(np.abs(stitched - wav))}"
+    dz.free(); dp.free(); dw.free()
+
+
+def test_stream_chunk_clipping_and_oracle(env):
+    """pt_v21_stream_chunk's argument rules (pt_v21_host.c:2874-2878): a < 0 reads as 0, win < 1
+    as 1, a window past the end is clipped, nothing left is an error; a clipped window's waveform
+    matches the oracle's decode of the same frames."""
+    ctx, model, ws, bs = env
+    say("stream chunk clipping")
+    lib = ctx.lib
+    T = 40
+    z = synth.latent(T, 41)
+    dz, dp = dev_of(ctx, z), pkg.DevBuf(256 * 64)
+    n = C.c_int64(-5)
+    assert lib.ptd_decode_chunk(ctx.ptr, model.ptr, dz.ptr, T, T, 8, dp.ptr, C.byref(n)) == -1
+    assert n.value == 0
+    assert lib.ptd_decode_chunk(ctx.ptr, model.ptr, dz.ptr, T, -3, 0, dp.ptr, C.byref(n)) == 0
+    assert n.value == 256
+    one = dp.download(ctx)[:256]
+    assert np.array_equal(one, _decode(ctx, model, np.ascontiguousarray(z[:, :1])))
+    assert np_ref.sndr(one, ol.decoder(ws, bs, np.ascontiguousarray(z[:, :1]))) >= 60.0
+    assert lib.ptd_decode_chunk(ctx.ptr, model.ptr, dz.ptr, T, 25, 64, dp.ptr, C.byref(n)) == 0
+    assert n.value == 256 * 15
+    got = dp.download(ctx)[:n.value]
+    ref = ol.decoder(ws, bs, np.ascontiguousarray(z[:, 25:]))
+    assert np_ref.sndr(got, ref) >= 60.0
+    dz.free(); dp.free()
+
+
 def test_config5_concurrent_streams_bitexact(env):
     """8 requests, T ~ U[56, 400], on 8 contexts/streams sharing one weight set: every stream's
     output equals the single-stream decode bit for bit, and one of them matches the oracle."""
