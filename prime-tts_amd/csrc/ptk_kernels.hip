@@ -655,6 +655,14 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
       return -1;
     }
     if (d->nq <= 0 || d->batch <= 0) continue;
+    // the kernel addresses one batch item's input rows and one row tile's weight panel through
+    // buffer resources with 32-bit byte ranges
+    if ((unsigned long long) d->cin * (unsigned long long) d->ldx * 4ull > 0xFFFFFFFFull ||
+        (unsigned long long) d->K * (unsigned long long) (d->cinp / CONV_CK) * 1024ull > 0xFFFFFFFFull) {
+      set_err("ptk_conv_launch: input rows (cin %d x ldx %lld) or weight panel (K %d) exceed the "
+              "4 GiB range of one buffer resource", d->cin, (long long) d->ldx, d->K);
+      return -1;
+    }
     if (d->in_op != PTK_IN_PLAIN && !(d->in_a >= 0.0f && d->in_a <= 1.0f)) {
       set_err("ptk_conv_launch: input LeakyReLU slope %g outside [0, 1]", (double) d->in_a);
       return -1;
