@@ -939,8 +939,10 @@ __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, 
     if (t >= 0 && t < L) {
       const float mag = expf(p[(long long) (b * 18 + k) * ldp + t]);
       const float ph = sinf(p[(long long) (b * 18 + 9 + k) * ldp + t]) * 3.1415927f;
-      re = mag * cosf(ph);
-      im = mag * sinf(ph);
+      float sn, cs;
+      sincosf(ph, &sn, &cs);
+      re = mag * cs;
+      im = mag * sn;
     }
     s_re[b][tt][k] = re;
     s_im[b][tt][k] = im;
@@ -982,15 +984,19 @@ __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, 
   }
   __syncthreads();
   // 4) PQMF synthesis: zero-insert x4 (gain 4), 63-tap FIR per band, sum of bands
+  // o0 is a multiple of 4, so tap m of output o reads y index (o + m - 31) >> 2, which is
+  // s_y[b][((tid + m - 31) >> 2) + 8]: the same slots for every block.  y outside [0, Ly) is
+  // stored as 0 above, so taps there add 0 and need no range test.
   const long long o = o0 + tid;
   if (o >= nout) return;
   float acc = 0.0f;
-  const int m0 = (int) ((31 - o) & 3);   // first tap with (o + m - 31) % 4 == 0
+  const int m0 = (31 - tid) & 3;                 // first tap with (o + m - 31) % 4 == 0
+  const int y0 = ((tid + m0 - 31) >> 2) + 8;     // its s_y slot; tap m0 + 4j reads y0 + j
   for (int b = 0; b < 4; b++) {
-    for (int m = m0; m < 63; m += 4) {
-      const long long i = (o + m - 31) >> 2;
-      if (i < 0 || i >= Ly) continue;
-      acc += h[b * 63 + m] * (4.0f * s_y[b][(int) (i - i_lo)]);
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      const int m = m0 + 4 * j;
+      if (m < 63) acc += h[b * 63 + m] * (4.0f * s_y[b][y0 + j]);
     }
   }
   if (o >= e_lo && o < e_hi) wav[o] = acc + hb[0];
