@@ -124,6 +124,19 @@ int ptd_decode_windows(pt_ctx *c, const ptd_model *m, const float *z, int64_t T,
                        float *wav);
 size_t ptd_windows_arena_bytes(int64_t T, int win, int ctx);
 
+/* A decode of fixed shape and buffers captured once as a HIP graph and replayed (no counterpart in
+ * the reference, whose graph interpreter issues every node from the host): for a serving loop that
+ * reuses its buffers, the 19 launches go to the device as one submission.  z and wav are read and
+ * written in place on every replay (refill z, launch, read wav).  The graph owns its scratch
+ * memory (ptd_decode_arena_bytes(T, batch)), so the context's arena is free for other work between
+ * replays.  Replays run on the capturing context's stream only; destroy the graph before the
+ * context and the model.  Launch is asynchronous; destroy waits for replays in flight. */
+typedef struct ptd_graph ptd_graph;
+ptd_graph *ptd_decode_graph(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int batch,
+                            float *wav);
+int ptd_graph_launch(pt_ctx *c, const ptd_graph *g);
+void ptd_graph_destroy(ptd_graph *g);
+
 /* One window of a sequence, for audio as it is decoded (replaces pt_v21_stream_chunk,
  * pt_v21.h:194, pt_v21_host.c:2871-2902): a < 0 reads as 0, win < 1 as 1, and the window is
  * clipped to [a, T); -1 if nothing is left.  pcm (device, >= 256*win floats) receives the whole

@@ -73,6 +73,9 @@ _SIGS = {
     "ptd_decode_windows": (C.c_int, [VP, VP, VP, I64, C.c_int, C.c_int, VP]),
     "ptd_windows_arena_bytes": (C.c_size_t, [I64, C.c_int, C.c_int]),
     "ptd_decode_chunk": (C.c_int, [VP, VP, VP, I64, I64, I64, VP, C.POINTER(I64)]),
+    "ptd_decode_graph": (VP, [VP, VP, VP, I64, C.c_int, VP]),
+    "ptd_graph_launch": (C.c_int, [VP, VP]),
+    "ptd_graph_destroy": (None, [VP]),
     "ptd_server_create": (VP, [C.c_int, C.c_size_t]),
     "ptd_server_destroy": (None, [VP]),
     "ptd_server_ctx": (VP, [VP, C.c_int]),

@@ -514,6 +514,68 @@ int ptd_decode_windows(pt_ctx *c, const ptd_model *m, const float *z, int64_t T,
   return rc;
 }
 
+/* ------------------------------------------------------------------ captured decodes
+ * A decode of fixed shape and buffers, recorded once as a HIP graph and replayed: its 19 launches
+ * then go to the device as one submission.  The capture runs against a scratch region the graph
+ * owns (the context's arena fields point at it for the duration), so replays never touch what the
+ * context keeps in its own arena. */
+struct ptd_graph {
+  pt_ctx *c;
+  void *exec, *scratch;
+};
+
+ptd_graph *ptd_decode_graph(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int batch,
+                            float *wav) {
+  if (!c || !c->use_cuda || !m || !z || !wav || T < 1 || batch < 1) return NULL;
+  ptd_graph *g = calloc(1, sizeof *g);
+  if (!g) return NULL;
+  g->c = c;
+  const size_t bytes = ptd_decode_arena_bytes(T, batch);
+  if (ptk_malloc(&g->scratch, bytes)) {
+    PT_LOG("ptd_decode_graph: %s", ptk_last_error());
+    free(g);
+    return NULL;
+  }
+  void *a0 = c->g_arena;
+  const size_t b0 = c->g_arena_bytes, u0 = c->g_arena_used, h0 = c->arena_alloc_bytes;
+  int rc = ptk_capture_begin(c->g_stream);
+  if (rc == 0) {
+    c->g_arena = g->scratch;
+    c->g_arena_bytes = bytes;
+    c->g_arena_used = 0;
+    rc = ptd_decode(c, m, z, T, batch, wav);
+    c->g_arena = a0;
+    c->g_arena_bytes = b0;
+    c->g_arena_used = u0;
+    c->arena_alloc_bytes = h0;
+    if (ptk_capture_end(c->g_stream, rc ? NULL : &g->exec)) rc = -1;
+  }
+  if (rc) {
+    PT_LOG("ptd_decode_graph: capture of a decode of T %lld x %d failed: %s", (long long) T, batch,
+           ptk_last_error());
+    ptd_graph_destroy(g);
+    return NULL;
+  }
+  return g;
+}
+
+int ptd_graph_launch(pt_ctx *c, const ptd_graph *g) {
+  if (!c || !g || !g->exec || c != g->c) return -1;
+  if (ptk_graph_launch(g->exec, c->g_stream)) {
+    PT_LOG("ptd_graph_launch: %s", ptk_last_error());
+    return -1;
+  }
+  return 0;
+}
+
+void ptd_graph_destroy(ptd_graph *g) {
+  if (!g) return;
+  if (g->exec || g->scratch) ptk_stream_sync(g->c->g_stream);   /* replays still running use both */
+  ptk_graph_destroy(g->exec);
+  ptk_free(g->scratch);
+  free(g);
+}
+
 /* One window at a time, for a caller that plays audio as it arrives (pt_v21_stream_chunk,
  * pt_v21_host.c:2871-2902): the same clipping of [a, a + win) to the sequence, and the window's
  * whole waveform (256 samples a frame) to pcm.  A batch-1 decode reading z in place. */

@@ -40,6 +40,12 @@ int ptk_stream_wait_event(void *s, void *e);
 int ptk_event_elapsed_ms(float *ms, void *e0, void *e1);
 int ptk_event_sync(void *e);
 int ptk_device_sync(void);
+/* Stream capture into a HIP graph (this thread's capture only) and replay.  ptk_capture_end ends
+ * the capture in every case; with exec == NULL (the captured work failed) it discards the graph. */
+int ptk_capture_begin(void *s);
+int ptk_capture_end(void *s, void **exec);
+int ptk_graph_launch(void *exec, void *s);
+int ptk_graph_destroy(void *exec);
 
 /* ---------------------------------------------------------------- conv problem descriptor
  * One implicit-GEMM problem.  Row m of the GEMM is an output channel (conv: m = co) or a phase

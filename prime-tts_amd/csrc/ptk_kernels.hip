@@ -156,6 +156,32 @@ extern "C" int ptk_device_sync(void) {
   HCHK(hipDeviceSynchronize());
   return 0;
 }
+extern "C" int ptk_capture_begin(void *s) {
+  HCHK(hipStreamBeginCapture((hipStream_t) s, hipStreamCaptureModeThreadLocal));
+  return 0;
+}
+extern "C" int ptk_capture_end(void *s, void **exec) {
+  hipGraph_t g = nullptr;
+  HCHK(hipStreamEndCapture((hipStream_t) s, &g));
+  if (!exec) {
+    if (g) (void) hipGraphDestroy(g);
+    return 0;
+  }
+  hipGraphExec_t e = nullptr;
+  const hipError_t err = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+  (void) hipGraphDestroy(g);
+  HCHK(err);
+  *exec = (void *) e;
+  return 0;
+}
+extern "C" int ptk_graph_launch(void *exec, void *s) {
+  HCHK(hipGraphLaunch((hipGraphExec_t) exec, (hipStream_t) s));
+  return 0;
+}
+extern "C" int ptk_graph_destroy(void *exec) {
+  if (exec) HCHK(hipGraphExecDestroy((hipGraphExec_t) exec));
+  return 0;
+}
 
 // ------------------------------------------------------------------------------ weight relayout
 // Packed [M/4][K][cin][4] (the reference's conv layout; a convT's phase rows are just more rows)

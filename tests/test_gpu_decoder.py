@@ -342,6 +342,41 @@ def test_stream_chunk_clipping_and_oracle(env):
     dz.free(); dp.free()
 
 
+def test_decode_graph_replays_match_eager(env):
+    """A decode captured as a HIP graph, replayed three times with eager decodes of another input
+    on the same context (its arena) and a synchronising read between the replays, gives the eager
+    decode's waveform bit for bit every time; refilling the input buffer makes the next replay
+    decode the new input; another context cannot launch it."""
+    ctx, model, ws, bs = env
+    say("decode graph replays")
+    lib = ctx.lib
+    T, To = 120, 200
+    z1, z2, zo = synth.latent(T, 61), synth.latent(T, 62), synth.latent(To, 63)
+    ref1, ref2 = _decode(ctx, model, z1), _decode(ctx, model, z2)
+    dz, dw = dev_of(ctx, z1), pkg.DevBuf(256 * T)
+    dzo, dwo = dev_of(ctx, zo), pkg.DevBuf(256 * To)
+    g = lib.ptd_decode_graph(ctx.ptr, model.ptr, dz.ptr, T, 1, dw.ptr)
+    assert g
+    try:
+        for _ in range(3):
+            dw.upload(ctx, np.full(256 * T, np.nan, np.float32))
+            assert lib.ptd_graph_launch(ctx.ptr, g) == 0
+            assert lib.ptd_decode(ctx.ptr, model.ptr, dzo.ptr, To, 1, dwo.ptr) == 0
+            assert np.array_equal(dw.download(ctx), ref1)
+        dz.upload(ctx, z2)
+        assert lib.ptd_graph_launch(ctx.ptr, g) == 0
+        assert np.array_equal(dw.download(ctx), ref2)
+        other = pkg.Ctx(arena_mb=64)
+        try:
+            assert lib.ptd_graph_launch(other.ptr, g) == -1
+        finally:
+            other.close()
+    finally:
+        lib.ptd_graph_destroy(g)
+    for b in (dz, dw, dzo, dwo):
+        b.free()
+
+
 def test_config5_concurrent_streams_bitexact(env):
     """8 requests, T ~ U[56, 400], on 8 contexts/streams sharing one weight set: every stream's
     output equals the single-stream decode bit for bit, and one of them matches the oracle."""
