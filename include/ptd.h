@@ -167,6 +167,10 @@ int ptd_serve_run(ptd_server *s, const ptd_model *m, const ptd_request *req, int
 /* ---- plumbing for callers without a HIP runtime of their own (tests, bench.py) ------------ */
 void *ptd_malloc(size_t bytes);                 /* device memory, NULL on failure */
 void ptd_free(void *p);
+/* Tests of the error paths (no counterpart in the reference, whose tests force failures through
+ * its env knobs only): after `skip` more device allocations of this library succeed, the next n
+ * fail as if the device were out of memory.  Process-wide; n = 0 switches it off. */
+void ptd_debug_fail_allocs(int skip, int n);
 int ptd_h2d(pt_ctx *c, void *dst, const void *src, size_t bytes);   /* synchronous */
 int ptd_d2h(pt_ctx *c, void *dst, const void *src, size_t bytes);   /* synchronous */
 int ptd_sync(pt_ctx *c);                        /* wait for the context's stream */

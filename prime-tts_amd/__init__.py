@@ -82,6 +82,7 @@ _SIGS = {
     "ptd_serve_run": (C.c_int, [VP, VP, VP, C.c_int, C.POINTER(C.c_double)]),
     "ptd_malloc": (VP, [C.c_size_t]),
     "ptd_free": (None, [VP]),
+    "ptd_debug_fail_allocs": (None, [C.c_int, C.c_int]),
     "ptd_h2d": (C.c_int, [VP, VP, VP, C.c_size_t]),
     "ptd_d2h": (C.c_int, [VP, VP, VP, C.c_size_t]),
     "ptd_sync": (C.c_int, [VP]),

@@ -301,6 +301,13 @@ static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t ld
                        int64_t T, int batch, float *wav, int64_t bsw, const ptk_emit *emit,
                        float *const *stages) {
   if (!c || !c->use_cuda || !m || !z || !wav || T < 1 || batch < 1) return -1;
+  /* refuse a decode the arena cannot hold before anything is queued */
+  const size_t need = ptd_decode_arena_bytes(T, batch);
+  if (c->g_arena_used > c->g_arena_bytes || need > c->g_arena_bytes - c->g_arena_used) {
+    PT_LOG("arena too small for a decode of T %lld x %d (need %zu MiB, %zu MiB free)",
+           (long long) T, batch, need >> 20, (c->g_arena_bytes - c->g_arena_used) >> 20);
+    return -1;
+  }
   const int64_t T1 = 4 * T, T2 = 16 * T, L = T2 + 1;
   const size_t f = sizeof(float) * (size_t) batch;
   void *mark = ptdi_arena_mark(c);

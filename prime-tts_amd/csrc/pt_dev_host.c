@@ -849,6 +849,7 @@ void *ptd_malloc(size_t bytes) {
   return p;
 }
 void ptd_free(void *p) { ptk_free(p); }
+void ptd_debug_fail_allocs(int skip, int n) { ptk_fail_allocs(skip, n); }
 int ptd_h2d(pt_ctx *c, void *dst, const void *src, size_t bytes) {
   if (!c || !c->use_cuda) return -1;
   return (ptk_h2d_async(dst, src, bytes, c->g_stream) || ptk_stream_sync(c->g_stream)) ? -1 : 0;

@@ -22,6 +22,7 @@ int ptk_stream_destroy(void *s);
 int ptk_stream_sync(void *s);
 int ptk_stream_query(void *s);                     /* 1 done, 0 busy, -1 error */
 int ptk_malloc(void **p, size_t bytes);
+void ptk_fail_allocs(int skip, int n);   /* tests: after skip more successes, n ptk_malloc calls fail */
 int ptk_free(void *p);
 int ptk_h2d_async(void *dst, const void *src, size_t bytes, void *s);
 int ptk_d2h_async(void *dst, const void *src, size_t bytes, void *s);

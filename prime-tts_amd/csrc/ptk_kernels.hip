@@ -88,7 +88,32 @@ extern "C" int ptk_stream_query(void *s) {
   set_err("hipStreamQuery: %s", hipGetErrorString(e));
   return -1;
 }
+// Failure injection for tests of the error paths: after `skip` more device allocations succeed,
+// the next `n` fail as if the device were out of memory (process-wide; nothing reaches the
+// device).  n = 0 switches it off.
+static std::mutex g_inject_lock;
+static int g_inject_skip, g_inject_fail;
+extern "C" void ptk_fail_allocs(int skip, int n) {
+  std::lock_guard<std::mutex> lk(g_inject_lock);
+  g_inject_skip = skip > 0 ? skip : 0;
+  g_inject_fail = n > 0 ? n : 0;
+}
+static bool inject_alloc_failure() {
+  std::lock_guard<std::mutex> lk(g_inject_lock);
+  if (g_inject_fail <= 0) return false;
+  if (g_inject_skip > 0) {
+    g_inject_skip--;
+    return false;
+  }
+  g_inject_fail--;
+  return true;
+}
 extern "C" int ptk_malloc(void **p, size_t bytes) {
+  if (inject_alloc_failure()) {
+    *p = nullptr;
+    set_err("hipMalloc(%zu bytes) failed: injected allocation failure", bytes);
+    return -1;
+  }
   HCHK(hipMalloc(p, bytes ? bytes : 1));
   return 0;
 }
