@@ -276,6 +276,18 @@ def main():
     lib.ptd_graph_destroy(graph)
     cfg["config4_graph_ms_per_request"] = round(ms4g, 4)
     cfg["config4_graph_audio_s_per_s_1stream"] = round(226 * HOP / SR / (ms4g * 1e-3), 2)
+    # the same request shape eight at a time in one batched decode (one stream): the kernels at
+    # fuller occupancy than one request gives them
+    z8 = pkg.DevBuf.of(ctx, np.concatenate([pkg.synth.latent(226, 226 + i) for i in range(8)]))
+    w8 = pkg.DevBuf(8 * HOP * 226)
+    f48 = lambda: lib.ptd_decode(ctx.ptr, model.ptr, z8.ptr, 226, 8, w8.ptr)  # noqa: E731
+    for _ in range(2):
+        f48()
+    ms48 = timer.time(f48, 10)
+    cfg["config4_batch8_ms"] = round(ms48, 4)
+    cfg["config4_batch8_decoder_tflops"] = round(8 * 32.571e9 / (ms48 * 1e-3) / 1e12, 3)
+    z8.free()
+    w8.free()
     for b in (dz, dh, dx0, dw):
         b.free()
     log(f"configs: {cfg}")

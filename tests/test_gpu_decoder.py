@@ -4,8 +4,10 @@ concurrent / long-form serving (config 5).
 
 Bars: per layer max |err| <= 1e-4 x RMS; end-to-end SNDR >= 60 dB.
 Size-independent properties at full size: 8 concurrent streams give bit-identical output to one
-stream (the kernels are deterministic), and the overlap-save windowed decode of T = 1500 stays
->= 60 dB from the full decode."""
+stream (the kernels are deterministic); a delayed input gives the exactly delayed output, per layer
+at the decoder's full shapes and through the whole decoder at T = 1500; batched items equal single
+decodes bit for bit; and the overlap-save windowed decode of T = 1500 stays >= 60 dB from the full
+decode."""
 from __future__ import annotations
 
 import ctypes as C
@@ -340,6 +342,61 @@ def test_stream_chunk_clipping_and_oracle(env):
     ref = ol.decoder(ws, bs, np.ascontiguousarray(z[:, 25:]))
     assert np_ref.sndr(got, ref) >= 60.0
     dz.free(); dp.free()
+
+
+# (layer, T, cin, rows of y, output columns per input column, half receptive field in input columns)
+# layers 18 / 19: MRF-256 K 11 c1 at dilation 5 and c2; 37: MRF-128 K 11 c1 at dilation 5
+_SHIFT_LAYERS = [(0, 226, 192, 512, 1, 3), (1, 226, 512, 256, 4, 4), (18, 904, 256, 256, 1, 25),
+                 (19, 904, 256, 256, 1, 5), (20, 904, 256, 128, 4, 4), (37, 3616, 128, 128, 1, 25),
+                 (39, 3616, 128, 72, 1, 3)]
+
+
+@pytest.mark.parametrize("layer,T,cin,rows,up,half", _SHIFT_LAYERS,
+                         ids=[f"layer{c[0]}-T{c[1]}" for c in _SHIFT_LAYERS])
+def test_layer_shift_equivariance_full_size(env, layer, T, cin, rows, up, half):
+    """At the decoder's full shapes (conv_pre and ups.0 at T = 226, MRF-256 at 904, ups.1 at 904,
+    MRF-128 and conv_post at 3616): an input delayed by s columns gives the output delayed by
+    up*s columns, bit for bit, wherever neither receptive field reaches an edge.  Each output
+    column is summed in the same order whichever tile holds it, so this checks every tile position
+    of the full-size grid without the oracle."""
+    ctx, model, ws, bs = env
+    s = 37
+    say(f"shift equivariance layer {layer} T={T}")
+    rng = np.random.default_rng(layer)
+    x = rng.standard_normal((cin, T)).astype(np.float32)
+    x2 = np.empty_like(x)
+    x2[:, s:] = x[:, :-s]
+    x2[:, :s] = rng.standard_normal((cin, s)).astype(np.float32)
+    lib = ctx.lib
+    outs = []
+    for xx in (x, x2):
+        dx, dy = dev_of(ctx, xx), pkg.DevBuf(rows * up * T + 64)
+        assert lib.ptd_layer(ctx.ptr, model.ptr, layer, dx.ptr, T, 1, dy.ptr, 0.1, 0.0) == 0
+        outs.append(dy.download(ctx)[:rows * up * T].reshape(rows, up * T))
+        dx.free(); dy.free()
+    y, y2 = outs
+    lo, hi = up * (s + half + 1), up * (T - half - 1)
+    assert hi - lo > up * T // 2
+    assert np.array_equal(y2[:, lo:hi], y[:, lo - up * s:hi - up * s])
+
+
+def test_decoder_shift_equivariance_T1500(env):
+    """The whole decoder at config 5's long-form length (T = 1500, too long for the oracle in a
+    test): latents delayed by s frames give the waveform delayed by 256*s samples, bit for bit,
+    away from both ends.  Every stage computes each column (sample) in an order that does not
+    depend on its position, so this holds exactly through all 19 launches."""
+    ctx, model, ws, bs = env
+    T, s, margin = 1500, 37, 48
+    say("decoder shift equivariance T=1500")
+    z = synth.latent(T, 1501)
+    z2 = np.empty_like(z)
+    z2[:, s:] = z[:, :-s]
+    z2[:, :s] = synth.latent(s, 1502)
+    w, w2 = _decode(ctx, model, z), _decode(ctx, model, z2)
+    lo, hi = 256 * (s + margin), 256 * (T - margin)
+    assert np.array_equal(w2[lo:hi], w[lo - 256 * s:hi - 256 * s])
+    # and the delay really is visible: the waveforms differ near the start
+    assert not np.array_equal(w2[:256 * s], w[:256 * s])
 
 
 def test_decode_graph_replays_match_eager(env):
