@@ -48,6 +48,36 @@ static int env_int(const char *name, int dflt) {
   return e && *e ? atoi(e) : dflt;
 }
 
+/* PT_V21_CUDAPROF (the reference's knob, pt_v21_cuda.cu:83-87, 1781-1955): each conv / convT /
+ * matmul call charges its device allocations to g_alloc_ms, its uploads to g_copy_ms, the
+ * kernels with the result copy and the stream wait to g_kernel_ms, and its frees to g_free_ms,
+ * synchronising the device between phases so each gets its own time.  Off, nothing is recorded
+ * and nothing extra is synchronised. */
+typedef struct {
+  int on;
+  double t;
+} phase_t;
+static int cudaprof(void) {
+  static int v = -1;   /* read once; a benign race between first callers */
+  if (v < 0) v = getenv("PT_V21_CUDAPROF") ? 1 : 0;
+  return v;
+}
+static void phase_begin(phase_t *p) {
+  p->on = cudaprof();
+  p->t = 0.0;
+  if (p->on) {
+    ptk_device_sync();
+    p->t = ptdi_now_ms();
+  }
+}
+static void phase_end(phase_t *p, double *field) {
+  if (!p->on) return;
+  ptk_device_sync();
+  const double t = ptdi_now_ms();
+  *field += t - p->t;
+  p->t = t;
+}
+
 /* ================================================================== weight pool */
 typedef struct {
   float *dev;
@@ -455,7 +485,8 @@ int pt_v21_conv(pt_ctx *c, const float *X, int64_t ldx, int64_t cin, float *Y, i
   const int keep = c->conv_keep;
   void *owned[5] = {NULL, NULL, NULL, NULL, NULL};
   int nown = 0;
-  const double t0 = ptdi_now_ms();
+  phase_t ph;
+  phase_begin(&ph);
 #define OWN_ALLOC(ptr, bytes)                                          \
   do {                                                                 \
     if (!(ptr)) {                                                      \
@@ -469,17 +500,22 @@ int pt_v21_conv(pt_ctx *c, const float *X, int64_t ldx, int64_t cin, float *Y, i
   if (!dx) {
     dxa = ptdi_arena_alloc(c, xb);
     OWN_ALLOC(dxa, xb);
+    phase_end(&ph, &c->g_alloc_ms);
     if (ptk_h2d_async(dxa, X, xb, c->g_stream)) goto fail;
+    phase_end(&ph, &c->g_copy_ms);
     dx = dxa;
   }
   dy = (keep && c->conv_keep_res) ? pt_v21_dev_alloc(c, yb) : ptdi_arena_alloc(c, yb);
   OWN_ALLOC(dy, yb);
+  phase_end(&ph, &c->g_alloc_ms);
   const float *rw = ptdi_pool_get(wtab, wb);
   const float *rb = bias ? ptdi_pool_get(btab, (size_t) cout * sizeof(float)) : NULL;
   if (bias && !rb) {
     db = ptdi_arena_alloc(c, (size_t) cout * sizeof(float));
     OWN_ALLOC(db, (size_t) cout * sizeof(float));
+    phase_end(&ph, &c->g_alloc_ms);
     if (ptk_h2d_async(db, bias, (size_t) cout * sizeof(float), c->g_stream)) goto fail;
+    phase_end(&ph, &c->g_copy_ms);
     rb = db;
   }
   ptk_conv_desc d;
@@ -492,7 +528,9 @@ int pt_v21_conv(pt_ctx *c, const float *X, int64_t ldx, int64_t cin, float *Y, i
     if (!rw) {
       dw = ptdi_arena_alloc(c, wb);
       OWN_ALLOC(dw, wb);
+      phase_end(&ph, &c->g_alloc_ms);
       if (ptk_h2d_async(dw, wp, wb, c->g_stream)) goto fail;
+      phase_end(&ph, &c->g_copy_ms);
       rw = dw;
     }
   }
@@ -502,6 +540,7 @@ int pt_v21_conv(pt_ctx *c, const float *X, int64_t ldx, int64_t cin, float *Y, i
       const size_t rb_bytes = ptk_relayout_floats(c4, K, (int) cin) * sizeof(float);
       dwr = ptdi_arena_alloc(c, rb_bytes);
       OWN_ALLOC(dwr, rb_bytes);
+      phase_end(&ph, &c->g_alloc_ms);
       if (ptk_relayout(dwr, rw, c4, K, (int) cin, c->g_stream)) goto fail;
       wr = dwr;
     }
@@ -517,7 +556,7 @@ int pt_v21_conv(pt_ctx *c, const float *X, int64_t ldx, int64_t cin, float *Y, i
     /* chain link: the next conv reads dy from the arena; released when the chain ends */
     if (!c->chain_mark) c->chain_mark = mark;
     c->conv_out_dev = dy;
-    c->g_kernel_ms += ptdi_now_ms() - t0;
+    phase_end(&ph, &c->g_kernel_ms);
     return 0;
   }
   if (ptdi_wait(c)) goto fail;
@@ -529,14 +568,15 @@ int pt_v21_conv(pt_ctx *c, const float *X, int64_t ldx, int64_t cin, float *Y, i
   }
   if (ptk_stream_sync(c->g_stream)) goto fail;
   pt_v21_dev_reclaim(c);
+  phase_end(&ph, &c->g_kernel_ms);
   for (int i = 0; i < nown; i++) ptk_free(owned[i]);
+  phase_end(&ph, &c->g_free_ms);
   if (c->chain_mark) {
     ptdi_arena_release(c, c->chain_mark);
     c->chain_mark = NULL;
   } else {
     ptdi_arena_release(c, mark);
   }
-  c->g_kernel_ms += ptdi_now_ms() - t0;
   return 0;
 fail:
   PT_LOG("pt_v21_conv failed: %s", ptk_last_error());
@@ -575,7 +615,8 @@ int pt_v21_convT(pt_ctx *c, const float *X, int64_t ldx, int64_t cin, int64_t ti
   void *mark = ptdi_arena_mark(c);
   void *owned[5] = {NULL, NULL, NULL, NULL, NULL};
   int nown = 0;
-  const double t0 = ptdi_now_ms();
+  phase_t ph;
+  phase_begin(&ph);
 #define OWN_ALLOC(ptr, bytes)                                          \
   do {                                                                 \
     if (!(ptr)) {                                                      \
@@ -586,22 +627,29 @@ int pt_v21_convT(pt_ctx *c, const float *X, int64_t ldx, int64_t cin, int64_t ti
   } while (0)
   float *dx = ptdi_arena_alloc(c, xb), *dy = NULL, *dw = NULL, *db = NULL, *dwr = NULL;
   OWN_ALLOC(dx, xb);
+  phase_end(&ph, &c->g_alloc_ms);
   if (ptk_h2d_async(dx, X, xb, c->g_stream)) goto fail;
+  phase_end(&ph, &c->g_copy_ms);
   dy = ptdi_arena_alloc(c, yb);
   OWN_ALLOC(dy, yb);
+  phase_end(&ph, &c->g_alloc_ms);
   const float *rw = ptdi_pool_get(wtab, wb);
   const float *rb = bias ? ptdi_pool_get(btab, (size_t) cout * sizeof(float)) : NULL;
   if (bias && !rb) {
     db = ptdi_arena_alloc(c, (size_t) cout * sizeof(float));
     OWN_ALLOC(db, (size_t) cout * sizeof(float));
+    phase_end(&ph, &c->g_alloc_ms);
     if (ptk_h2d_async(db, bias, (size_t) cout * sizeof(float), c->g_stream)) goto fail;
+    phase_end(&ph, &c->g_copy_ms);
     rb = db;
   }
   const int resident = rw != NULL;
   if (!rw) {
     dw = ptdi_arena_alloc(c, wb);
     OWN_ALLOC(dw, wb);
+    phase_end(&ph, &c->g_alloc_ms);
     if (ptk_h2d_async(dw, wp, wb, c->g_stream)) goto fail;
+    phase_end(&ph, &c->g_copy_ms);
     rw = dw;
   }
   ptk_conv_desc d;
@@ -613,6 +661,7 @@ int pt_v21_convT(pt_ctx *c, const float *X, int64_t ldx, int64_t cin, int64_t ti
       const size_t rbytes = ptk_relayout_floats(s * c4, ntap, (int) cin) * sizeof(float);
       dwr = ptdi_arena_alloc(c, rbytes);
       OWN_ALLOC(dwr, rbytes);
+      phase_end(&ph, &c->g_alloc_ms);
       if (ptk_relayout(dwr, rw, s * c4, ntap, (int) cin, c->g_stream)) goto fail;
       wr = dwr;
     }
@@ -630,9 +679,10 @@ int pt_v21_convT(pt_ctx *c, const float *X, int64_t ldx, int64_t cin, int64_t ti
     goto fail;
   }
   if (ptk_stream_sync(c->g_stream)) goto fail;
+  phase_end(&ph, &c->g_kernel_ms);
   for (int i = 0; i < nown; i++) ptk_free(owned[i]);
   ptdi_arena_release(c, mark);
-  c->g_kernel_ms += ptdi_now_ms() - t0;
+  phase_end(&ph, &c->g_free_ms);
   return 0;
 fail:
   PT_LOG("pt_v21_convT failed: %s", ptk_last_error());
@@ -671,6 +721,8 @@ int pt_v21_matmul(pt_ctx *c, const float *A, int64_t m, int64_t k, int64_t lda, 
   if (ldc != nn && !(hC = malloc(cb))) { free(hA); free(hB); return fail_oom("pt_v21_matmul"); }
   for (int64_t i = 0; hA && i < m; i++) memcpy(hA + i * k, A + i * lda, (size_t) k * f);
   for (int64_t i = 0; hB && i < k; i++) memcpy(hB + i * nn, B + i * ldb, (size_t) nn * f);
+  phase_t ph;
+  phase_begin(&ph);
   void *mark = ptdi_arena_mark(c);
   float *dA = ptdi_arena_alloc(c, ab), *dB = ptdi_arena_alloc(c, bb), *dC = ptdi_arena_alloc(c, cb);
   int own = 0;
@@ -685,12 +737,15 @@ int pt_v21_matmul(pt_ctx *c, const float *A, int64_t m, int64_t k, int64_t lda, 
     }
     own = 1;
   }
-  int r = (k > 0 && (ptk_h2d_async(dA, hA ? hA : A, (size_t) m * k * f, c->g_stream) ||
-                     ptk_h2d_async(dB, hB ? hB : B, (size_t) k * nn * f, c->g_stream))) ||
-          ptk_matmul(dA, m, k, k, dB, nn, nn, dC, nn, c->g_stream) || ptdi_wait(c) ||
-          ptk_d2h_async(hC ? hC : C, dC, cb, c->g_stream) || ptk_stream_sync(c->g_stream);
+  phase_end(&ph, &c->g_alloc_ms);
+  int r = k > 0 && (ptk_h2d_async(dA, hA ? hA : A, (size_t) m * k * f, c->g_stream) ||
+                    ptk_h2d_async(dB, hB ? hB : B, (size_t) k * nn * f, c->g_stream));
+  phase_end(&ph, &c->g_copy_ms);
+  r = r || ptk_matmul(dA, m, k, k, dB, nn, nn, dC, nn, c->g_stream) || ptdi_wait(c) ||
+      ptk_d2h_async(hC ? hC : C, dC, cb, c->g_stream) || ptk_stream_sync(c->g_stream);
   if (!r && hC)
     for (int64_t i = 0; i < m; i++) memcpy(C + i * ldc, hC + i * nn, (size_t) nn * f);
+  phase_end(&ph, &c->g_kernel_ms);
   if (r) PT_LOG("pt_v21_matmul failed: %s", ptk_last_error());
   if (own) {
     ptk_free(dA); ptk_free(dB); ptk_free(dC);
@@ -698,6 +753,7 @@ int pt_v21_matmul(pt_ctx *c, const float *A, int64_t m, int64_t k, int64_t lda, 
     ptdi_arena_release(c, mark);
   }
   free(hA); free(hB); free(hC);
+  phase_end(&ph, &c->g_free_ms);
   return r ? -1 : 0;
 }
 

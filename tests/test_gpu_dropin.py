@@ -83,6 +83,29 @@ def test_reference_driver_through_the_library(model, tmp_path, mode):
     assert "pt_v21 hip: context ready" in r.stderr
 
 
+def test_reference_driver_gpu_split(model, tmp_path):
+    """PT_V21_CUDAPROF=1, the reference's phase profiler: the linked driver prints its own
+    "gpu split" line from the context fields this library fills (alloc / copy / kernel+sync /
+    free per call, the device synchronised between phases), the phases are all non-negative, the
+    uploads and the kernels take time, and their sum stays within the driver's own total for the
+    conv / convT / matmul calls.  The waveform still passes the driver's gate."""
+    d, case, _ = model
+    say("reference driver with PT_V21_CUDAPROF=1")
+    r = _run([DEV_BIN, "--container", d / "model.ptk", "--case", case, "--out", tmp_path / "w.npy"],
+             300, {"PT_V21_CUDAPROF": "1"})
+    assert r.returncode == 0
+    m = re.search(r"gpu split: alloc ([0-9.]+) ms\s+copy ([0-9.]+) ms\s+kernel\+sync ([0-9.]+) ms"
+                  r"\s+free ([0-9.]+) ms", r.stderr)
+    assert m, r.stderr[-2000:]
+    alloc, copy, kern, free = (float(v) for v in m.groups())
+    say(f"gpu split: alloc {alloc} copy {copy} kernel+sync {kern} free {free} ms")
+    assert min(alloc, copy, kern, free) >= 0.0 and copy > 0.0 and kern > 0.0
+    t = re.search(r"conv ([0-9.]+) ms\s+convT ([0-9.]+) ms\s+matmul ([0-9.]+) ms", r.stdout)
+    assert t, r.stdout[-2000:]
+    total = sum(float(v) for v in t.groups())
+    assert alloc + copy + kern + free <= total * 1.05 + 1.0
+
+
 @pytest.mark.skipif(not PAR_BIN.exists(), reason="oracle/_ref/pt_v21_par_mi355x not built")
 def test_reference_multistream_driver(model):
     d, case, _ = model
