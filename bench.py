@@ -170,7 +170,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the decoder path shards by request with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(the decoder path would shard by request, with no exchange between GPUs)", file=sys.stderr)
         sys.exit(2)
 
     pkg = _package()
