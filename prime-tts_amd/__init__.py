@@ -16,7 +16,8 @@ import numpy as np
 from . import synth  # noqa: F401
 
 HERE = pathlib.Path(__file__).resolve().parent
-LIB_PATH = HERE / "libptconv_hip.so"
+# PTD_LIB: another build of the same library (e.g. the host AddressSanitizer build, `make asan`)
+LIB_PATH = pathlib.Path(os.environ["PTD_LIB"]) if os.environ.get("PTD_LIB") else HERE / "libptconv_hip.so"
 
 F = C.POINTER(C.c_float)
 I64 = C.c_int64
