@@ -6,8 +6,9 @@ One step = BASELINE config 5, the largest single-GPU configuration: 8 independen
 long-form request of T = 1500 frames through 96-frame overlap-save windows with 16-frame context
 on a ninth context, all sharing one uploaded weight set.  Inputs are resident in HBM before the
 timed region; `value` is the step's audio seconds divided by its wall time.  Alongside: config 4
-(one request, T = 226) on one stream, the long-form request window by window (time to first
-audio) and batched, configs 1-3 in TFLOP/s, the dominant kernel against the
+(one request, T = 226) on one stream, eager, replayed as a HIP graph and eight at a time, the
+long-form request window by window (time to first audio) and batched, the container load and
+pt_v21_matmul, configs 1-3 in TFLOP/s, the dominant kernel against the
 fp32-MFMA roofline (HIP events on the stream it runs on), and the reference's CPU conv path timed
 on this host on a bounded sample.
 
@@ -292,6 +293,49 @@ def main():
         b.free()
     log(f"configs: {cfg}")
 
+    # ---------------------------------------------------------------- the container path and the
+    # matmul entry point (the last two scope rows): the decoder's records written as the
+    # reference's exporter writes them (fp16 layers), then opened, parsed, uploaded as fp16,
+    # expanded and relaid on the device; and pt_v21_matmul at the encoder's attention shapes with
+    # host buffers, as the reference's interpreter calls it
+    sys.path.insert(0, str(ROOT / "tests"))
+    import tempfile
+    import ptk_writer as pw
+    with tempfile.TemporaryDirectory() as td:
+        path = pathlib.Path(td) / "decoder.ptk"
+        pw.write(path, pw.decoder_tensors(ws, bs, half=True))
+        size = path.stat().st_size
+        t0 = time.perf_counter()
+        ptk = pkg.Ptk(path)
+        t1 = time.perf_counter()
+        model2 = pkg.Model.from_ptk(ctx, ptk)
+        ctx.sync()
+        t2 = time.perf_counter()
+        nrec = int(lib.ptd_ptk_count(ptk.ptr))
+        ptk.close()
+        model2.close()
+    container = {"file_mb": round(size / 1e6, 3), "records": nrec,
+                 "open_parse_ms": round((t1 - t0) * 1e3, 2),
+                 "model_create_ms": round((t2 - t1) * 1e3, 2),
+                 "total_ms": round((t2 - t0) * 1e3, 2)}
+    log(f"container load: {container}")
+    mm = {}
+    for m_, k_, n_ in [(37, 53, 29), (120, 192, 120), (120, 96, 192)]:
+        rngm = np.random.default_rng(m_ + k_ + n_)
+        A = rngm.standard_normal((m_, k_)).astype(np.float32)
+        B = rngm.standard_normal((k_, n_)).astype(np.float32)
+        Cm = np.zeros((m_, n_), np.float32)
+        fmm = lambda: lib.pt_v21_matmul(ctx.ptr, pkg.fptr(A), m_, k_, k_, pkg.fptr(B), n_, n_,  # noqa: E731
+                                        pkg.fptr(Cm), n_)
+        for _ in range(3):
+            if fmm() != 0:
+                raise RuntimeError("pt_v21_matmul failed")
+        t0 = time.perf_counter()
+        for _ in range(50):
+            fmm()
+        mm[f"{m_}x{k_}x{n_}"] = round((time.perf_counter() - t0) / 50 * 1e6, 1)
+    log(f"pt_v21_matmul us per call (host buffers): {mm}")
+
     # ---------------------------------------------------------------- streaming (config 5's
     # long-form request on one stream): the first 96-frame window alone (time to first audio),
     # every window one at a time as the reference's --stream driver issues them, and the batched
@@ -394,6 +438,8 @@ def main():
             "alg_bytes_per_request": tail_bytes(TAIL_L, 1), **tail,
         },
         "streaming": stream,
+        "container_load": container,
+        "matmul_us_per_call": mm,
         **cfg,
     }
     if not args.no_cpu_baseline:
