@@ -42,15 +42,17 @@ def _run(cmd, timeout, env=None):
     return r
 
 
-@pytest.fixture(scope="module")
-def model(tmp_path_factory):
-    """A synthetic full model, a 40-token case, and the reference CPU build's waveform for it
-    (stored as the case's wav.npy, which the drivers compare against)."""
-    d = tmp_path_factory.mktemp("dropin")
-    say("synthetic full model + 40-token case")
+@pytest.fixture(scope="module", params=[40, 97], ids=lambda n: f"{n}tok")
+def model(tmp_path_factory, request):
+    """A synthetic full model, a 40- or 97-token case (different frame counts through the whole
+    graph), and the reference CPU build's waveform for it (stored as the case's wav.npy, which
+    the drivers compare against)."""
+    n_tokens = request.param
+    d = tmp_path_factory.mktemp(f"dropin{n_tokens}")
+    say(f"synthetic full model + {n_tokens}-token case")
     fm.write_container(d / "model.ptk", seed=0)
     case = d / "case"
-    fm.write_case(case, n_tokens=40, seed=0)
+    fm.write_case(case, n_tokens=n_tokens, seed=n_tokens)
     cpu_wav = d / "cpu.npy"
     say("reference CPU build")
     _run([CPU_BIN, "--cpu", "--container", d / "model.ptk", "--case", case, "--out", cpu_wav], 600)
