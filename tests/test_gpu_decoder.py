@@ -236,7 +236,7 @@ def test_windows_small_vs_oracle(env):
 
 
 @pytest.mark.parametrize("T,win,cx", [(20, 32, 8), (32, 32, 8), (48, 32, 8), (57, 32, 8), (70, 32, 8),
-                                      (100, 40, 4)])
+                                      (100, 40, 4), (50, 16, 0)])
 def test_windows_schedule_edges_bitexact(env, T, win, cx):
     """The windowed decode (one batched decode reading the latents in place, each window's kept
     frames written straight to the output) equals per-window single decodes stitched by the
@@ -281,7 +281,7 @@ def test_config5_longform_windows_vs_full(env):
     dz.free(); dw.free()
 
 
-@pytest.mark.parametrize("T,win,cx", [(20, 32, 8), (57, 32, 8), (70, 32, 8), (300, 96, 16)])
+@pytest.mark.parametrize("T,win,cx", [(20, 32, 8), (57, 32, 8), (70, 32, 8), (300, 96, 16), (50, 16, 0)])
 def test_stream_chunks_stitched_equal_windows(env, T, win, cx):
     """ptd_decode_chunk window by window, stitched the way the reference's --stream driver does
     (main_v21.c:341-362: step win - 2*ctx, keep [ctx, win_eff - ctx) frames of each window, the
