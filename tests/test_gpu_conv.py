@@ -259,7 +259,8 @@ def test_pool_resident_weights(ctx):
 
 
 @pytest.mark.parametrize("m,k,n,pad", [(37, 53, 29, 0), (120, 192, 120, 0), (120, 96, 192, 0),
-                                       (70, 13, 65, 3), (5, 0, 7, 1)])
+                                       (70, 13, 65, 3), (5, 0, 7, 1), (1, 1, 1, 0), (65, 129, 33, 2),
+                                       (3, 1000, 7, 0), (64, 8, 64, 0), (129, 7, 1, 5)])
 def test_matmul(ctx, m, k, n, pad):
     """pt_v21_matmul (fp32 MFMA) against float64, with tight and padded leading dimensions
     (lda = k + pad, ldb = ldc = n + pad) and the k = 0 case (C = 0)."""
