@@ -133,7 +133,8 @@ int ptk_convT_simt(const float *x, int64_t ldx, int64_t bsx, int64_t tin, int ci
                    const float *wp, const float *bias, int cout, int st, int pad, int K, float *y,
                    int64_t ldy, int64_t bsy, int64_t Lout, int batch, void *s);
 
-/* C[m][nn] = A[m][k] @ B[k][nn], row strides lda/ldb/ldc; one thread per output, p ascending */
+/* C[m][nn] = A[m][k] @ B[k][nn], row strides lda/ldb/ldc, on fp32 MFMA: a 64 x 64 block of C per
+ * workgroup, 32 x 32 per wave, k in steps of 8 (out-of-range rows, columns and k read as 0) */
 int ptk_matmul(const float *A, int64_t m, int64_t k, int64_t lda, const float *B, int64_t ldb,
                int64_t nn, float *C, int64_t ldc, void *s);
 
