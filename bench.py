@@ -222,7 +222,7 @@ def main():
 
     # ---------------------------------------------------------------- narrow late stages (GB/s)
     tail = {}
-    for batch in (1, 8):
+    for batch in (1, 8, 64):
         tp, tw = tail_setup(pkg, ctx, TAIL_L, batch)
         ft = lambda: lib.ptd_tail(ctx.ptr, model.ptr, tp.ptr, TAIL_L, batch, tw.ptr)  # noqa: E731
         ft()
