@@ -949,13 +949,14 @@ extern "C" int ptk_leaky(const float *a, float *y, int64_t n, float alpha, void 
 //   wav[o] = sum_b sum_m h[b][m] * 4 * y[b][(o+m-31)/4]   over (o+m-31) = 0 mod 4 in range.
 // One workgroup produces TAIL_OUT consecutive samples; it recomputes the ~TAIL_OUT/16 + 5 frames
 // per band it needs (in LDS), so the whole tail is a single pass over p with no intermediates.
-#define TAIL_OUT 256
-// phase 4 maps thread t of a block to output o0 + t: one output per thread, the whole block
-static_assert(TAIL_OUT == 256, "tail_kernel runs 256 threads, one per output sample");
+#define TAIL_OUT 512
+// phase 4 maps thread t of a block to output o0 + t: one output per thread, TAIL_OUT threads.
+// 512 measured best: 256 recomputes more frames per output (26 for 16), 1024 leaves most CUs idle
+// at batch 1 (57 blocks for one T = 226 request)
 #define TAIL_NY (TAIL_OUT / 4 + 18)
 #define TAIL_NT (TAIL_NY / 4 + 6)
 
-__global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, long long ldp,
+__global__ void __launch_bounds__(TAIL_OUT) tail_kernel(const float *__restrict__ p, long long ldp,
                                                     long long bsp, long long L,
                                                     float *__restrict__ wav, long long bsw,
                                                     const float *__restrict__ cst, ptk_emit em) {
@@ -968,7 +969,7 @@ __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, 
   __shared__ float s_fr[4][TAIL_NT][16];
   __shared__ float s_y[4][TAIL_NY];
   const int tid = threadIdx.x;
-  for (int i = tid; i < PTK_TAIL_NCONST; i += 256) s_c[i] = cst[i];
+  for (int i = tid; i < PTK_TAIL_NCONST; i += TAIL_OUT) s_c[i] = cst[i];
   const float *hann = s_c, *bc = s_c + 16, *bs = s_c + 160, *h = s_c + 304, *hb = s_c + 556;
   const long long Ly = 4 * (L - 1);
   const long long nout = 4 * Ly;
@@ -983,7 +984,7 @@ __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, 
   __syncthreads();
   // 1) spectra of the needed frames; consecutive threads take consecutive frames of one
   //    (band, bin) row, so the reads of p are coalesced
-  for (int e = tid; e < 4 * 9 * TAIL_NT; e += 256) {
+  for (int e = tid; e < 4 * 9 * TAIL_NT; e += TAIL_OUT) {
     const int tt = e % TAIL_NT, bk = e / TAIL_NT, b = bk / 9, k = bk % 9;
     const long long t = t_lo + tt;
     float re = 0.0f, im = 0.0f;
@@ -1000,7 +1001,7 @@ __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, 
   }
   __syncthreads();
   // 2) windowed frames (irfft through the basis)
-  for (int e = tid; e < 4 * TAIL_NT * 16; e += 256) {
+  for (int e = tid; e < 4 * TAIL_NT * 16; e += TAIL_OUT) {
     const int b = e / (TAIL_NT * 16), rem = e % (TAIL_NT * 16), tt = rem / 16, n = rem % 16;
     float fr = 0.0f, fi = 0.0f;
 #pragma unroll
@@ -1012,7 +1013,7 @@ __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, 
   }
   __syncthreads();
   // 3) overlap-add, window-sum normalisation, [8:-8] trim
-  for (int e = tid; e < 4 * TAIL_NY; e += 256) {
+  for (int e = tid; e < 4 * TAIL_NY; e += TAIL_OUT) {
     const int b = e / TAIL_NY, ii = e % TAIL_NY;
     const long long i = i_lo + ii;
     float yv = 0.0f;
@@ -1065,7 +1066,7 @@ extern "C" int ptk_tail_batched(const float *p, int64_t ldp, int64_t bsp, int64_
   const ptk_emit all = {0, 0, nout, nout};
   const ptk_emit em = emit ? *emit : all;
   const unsigned blocks = (unsigned) ((nout + TAIL_OUT - 1) / TAIL_OUT);
-  hipLaunchKernelGGL(tail_kernel, dim3(blocks, (unsigned) batch), dim3(256), 0, (hipStream_t) s, p,
+  hipLaunchKernelGGL(tail_kernel, dim3(blocks, (unsigned) batch), dim3(TAIL_OUT), 0, (hipStream_t) s, p,
                      (long long) ldp, (long long) bsp, (long long) L, wav, (long long) bsw, consts, em);
   HCHK(hipGetLastError());
   return 0;
