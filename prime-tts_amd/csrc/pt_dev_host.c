@@ -11,6 +11,7 @@
 #define _GNU_SOURCE
 #include <pthread.h>
 #include <sched.h>
+#include <sys/prctl.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -267,20 +268,32 @@ void ptdi_arena_release(pt_ctx *c, void *mark) {
 /* ================================================================== wait policy
  * PT_V21_WAIT_US = 0 (default): the runtime's own stream wait.  > 0: poll the stream, sleeping
  * that long between polls while another context is doing host work (the reference's policy for
- * few-core hosts, pt_v21_cuda.cu:25-57), yielding otherwise. */
+ * few-core hosts, pt_v21_cuda.cu:25-57, whose default is 200), yielding otherwise;
+ * PT_V21_WAIT_ADAPT=0 always sleeps.  The default differs from the reference's because an MI355X
+ * host has cores to spare for the runtime's own wait. */
 static volatile int g_n_active, g_n_waiting;
 
 void pt_v21_cuda_active(int delta) { __sync_add_and_fetch(&g_n_active, delta); }
 
 int ptdi_wait(pt_ctx *c) {
-  static int wait_us = -1;
-  if (wait_us < 0) wait_us = env_int("PT_V21_WAIT_US", 0);
+  static int wait_us = -1, adapt = 1;   /* read once; a benign race between first callers */
+  if (wait_us < 0) {
+    adapt = env_int("PT_V21_WAIT_ADAPT", 1);
+    wait_us = env_int("PT_V21_WAIT_US", 0);
+  }
   if (wait_us <= 0) return ptk_stream_sync(c->g_stream);
+  /* the default 50 us timer slack would stretch each short poll sleep (PT_V21_SLACK0 keeps it) */
+  static __thread int slack_set;
+  if (!slack_set) {
+    if (!getenv("PT_V21_SLACK0")) prctl(PR_SET_TIMERSLACK, 1UL, 0, 0, 0);
+    slack_set = 1;
+  }
   const struct timespec ts = {0, (long) wait_us * 1000L};
   __sync_add_and_fetch(&g_n_waiting, 1);
   int r;
   while ((r = ptk_stream_query(c->g_stream)) == 0) {
-    if (__sync_add_and_fetch(&g_n_active, 0) - __sync_add_and_fetch(&g_n_waiting, 0) <= 0)
+    /* sleep only while another context does host work; when every one waits, yield-poll */
+    if (adapt && __sync_add_and_fetch(&g_n_active, 0) - __sync_add_and_fetch(&g_n_waiting, 0) <= 0)
       sched_yield();
     else
       nanosleep(&ts, NULL);

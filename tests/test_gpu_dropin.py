@@ -109,10 +109,15 @@ def test_reference_driver_gpu_split(model, tmp_path):
 
 
 @pytest.mark.skipif(not PAR_BIN.exists(), reason="oracle/_ref/pt_v21_par_mi355x not built")
-def test_reference_multistream_driver(model):
+@pytest.mark.parametrize("wait", [{}, {"PT_V21_WAIT_US": "200"},
+                                  {"PT_V21_WAIT_US": "200", "PT_V21_WAIT_ADAPT": "0"}],
+                         ids=["runtime-wait", "sleep-poll-200us", "sleep-poll-always"])
+def test_reference_multistream_driver(model, wait):
+    """8 concurrent streams under the driver's own gate, with the runtime's stream wait and with
+    the reference's sleep-poll wait policy (its default 200 us, adaptive or always sleeping)."""
     d, case, _ = model
     say("reference multi-stream driver, 8 streams")
-    rp = _run([PAR_BIN, "--container", d / "model.ptk", "--case", case, "--parallel", 8], 300)
+    rp = _run([PAR_BIN, "--container", d / "model.ptk", "--case", case, "--parallel", 8], 300, wait)
     # the driver's own gate: every stream >= 60 dB against the CPU build's waveform
     assert rp.returncode == 0, rp.stdout + rp.stderr
     sndrs = [float(v) for v in re.findall(r"stream \d+: L=\d+ .*?SNDR=([0-9.]+) dB", rp.stdout)]
