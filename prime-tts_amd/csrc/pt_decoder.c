@@ -506,15 +506,17 @@ int ptd_decode_windows(pt_ctx *c, const ptd_model *m, const float *z, int64_t T,
     free(ws);
     return -1;
   }
-  if (nfull) {
-    const ptk_emit em = {0, (int64_t) ctx * 256, (int64_t) (win - ctx) * 256,
-                         (int64_t) (nfull == n ? win : win - ctx) * 256};
-    rc = decode_impl(c, m, z, T, hop, win, nfull, wav, hop * 256, &em, NULL);
-  }
-  if (rc == 0 && nfull < n) {   /* the shorter last window */
+  /* the shorter last window first: a small decode that leaves most of the chip to other streams
+   * is better early than as the tail of the request (the windows write disjoint samples) */
+  if (nfull < n) {
     const win_t *l = &ws[n - 1];
     const ptk_emit em = {(l->e0 - l->a) * 256, 0, (l->e1 - l->a) * 256, (l->e1 - l->a) * 256};
     rc = decode_impl(c, m, z + l->a, T, 0, l->w, 1, wav + l->a * 256, 0, &em, NULL);
+  }
+  if (rc == 0 && nfull) {
+    const ptk_emit em = {0, (int64_t) ctx * 256, (int64_t) (win - ctx) * 256,
+                         (int64_t) (nfull == n ? win : win - ctx) * 256};
+    rc = decode_impl(c, m, z, T, hop, win, nfull, wav, hop * 256, &em, NULL);
   }
   if (rc) PT_LOG("windowed decode failed: %s", ptk_last_error());
   free(ws);
