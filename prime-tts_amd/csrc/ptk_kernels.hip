@@ -706,13 +706,11 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
       return -1;
     }
     if (d->nq <= 0 || d->batch <= 0) continue;
-    // the kernel addresses one batch item's input rows and one row tile's weight panel through
-    // buffer resources; padding reads use the PTK_OOB offset (2 GiB), which reads 0 only while
-    // the buffer is smaller than that
-    if ((unsigned long long) d->cin * (unsigned long long) d->ldx * 4ull >= (unsigned long long) PTK_OOB ||
-        (unsigned long long) d->K * (unsigned long long) (d->cinp / CONV_CK) * 1024ull >= (unsigned long long) PTK_OOB) {
-      set_err("ptk_conv_launch: input rows (cin %d x ldx %lld) or weight panel (K %d) reach the "
-              "2 GiB range of one buffer resource", d->cin, (long long) d->ldx, d->K);
+    // a row tile's weight panel is addressed through one buffer resource (the input rows are
+    // bounded the same way by ptk_conv_mfma_ok)
+    if ((unsigned long long) d->K * (unsigned long long) (d->cinp / CONV_CK) * 1024ull >= (unsigned long long) PTK_OOB) {
+      set_err("ptk_conv_launch: weight panel (K %d, cin %d) reaches the 2 GiB range of one buffer "
+              "resource", d->K, d->cin);
       return -1;
     }
     if (d->in_op != PTK_IN_PLAIN && !(d->in_a >= 0.0f && d->in_a <= 1.0f)) {
