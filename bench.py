@@ -141,6 +141,7 @@ def cpu_baseline(pkg):
     ol.decoder(ws, bs, z, use_ref=use_ref)
     dt1 = time.perf_counter() - t0
     audio1 = T * HOP / SR
+    layers = _cpu_layers(pkg, ol, ws, bs, use_ref, cores[0])
     return {"value": round(audio8 / dt8, 4), "unit": "audio-s/s", "cores": nthr, "kind": kind,
             "sample": f"config 5's 8 requests (T={Ts}, {audio8:.2f} s audio; the T=1500 long-form "
                       f"request not included) as {nthr} threads pinned to cores {cores[:nthr]}: "
@@ -148,7 +149,41 @@ def cpu_baseline(pkg):
             "single_thread": {"value": round(audio1 / dt1, 4), "unit": "audio-s/s", "cores": 1,
                               "sample": f"one config-4 decode (T=226, {audio1:.3f} s audio) on 1 "
                                         f"thread: {dt1:.2f} s"},
-            "host_cpus": len(cores), "model": _cpu_model()}
+            "configs_1_3_single_thread": layers,
+            "host_cpus": len(cores), "nproc": os.cpu_count(), "model": _cpu_model()}
+
+
+def _cpu_layers(pkg, ol, ws, bs, use_ref, core):
+    """Configs 1-3 through the same CPU conv path on one thread pinned to one core, with the
+    weights and inputs the GPU legs of configs 1-3 use.  The LeakyReLU in front of config 2's
+    convT and the MRF glue run inside the timed region as the host ops they are in the
+    reference's interpreter."""
+    lib = ol.ref() if use_ref else None
+    z = pkg.synth.latent(226, 226)
+    prev = os.sched_getaffinity(0)
+    os.sched_setaffinity(0, {core})
+    try:
+        out = {}
+        t0 = time.perf_counter()
+        h = ol.conv(z, ws[0], bs[0], 512, 7, 1, 3, 1, epi0=1, a0=0.1, lib=lib)
+        dt = time.perf_counter() - t0
+        out["config1_conv_gflops"] = round(2 * 512 * 192 * 7 * 226 / dt / 1e9, 3)
+        t0 = time.perf_counter()
+        hl = np.where(h >= 0, h, np.float32(0.1) * h).astype(np.float32)
+        ol.convT(hl, ws[1], bs[1], 256, 16, 4, 6, lib=lib)
+        dt = time.perf_counter() - t0
+        out["config2_convT_gflops"] = round(2 * 256 * 512 * 4 * 904 / dt / 1e9, 3)
+        for first, (C_, T) in ((2, (256, 904)), (21, (128, 3616))):
+            x = np.random.default_rng(5).standard_normal((C_, T)).astype(np.float32)
+            t0 = time.perf_counter()
+            ol.mrf(ws[first:first + 18], bs[first:first + 18], x, 0.1, use_ref=use_ref)
+            dt = time.perf_counter() - t0
+            out[f"config3_mrf{C_}_gflops"] = round(2 * C_ * C_ * T * 126 / dt / 1e9, 3)
+    finally:
+        os.sched_setaffinity(0, prev)
+    out["cores"] = 1
+    out["core"] = core
+    return out
 
 
 def _cpu_model():

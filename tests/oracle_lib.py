@@ -185,14 +185,21 @@ def decoder_threads(ws, bs, zs, cores, use_ref=False):
     return wavs, dt
 
 
-def mrf(wts, bts, x, alpha):
+def mrf(wts, bts, x, alpha, use_ref=False):
     lib = oracle()
-    C_, T = x.shape
-    out = np.zeros_like(x)
-    wa = (F * 18)(*[fptr(w) for w in wts])
-    ba = (F * 18)(*[fptr(b) for b in bts])
-    rc = lib.orc_mrf(wa, ba, C_, T, fptr(np.ascontiguousarray(x)), alpha, fptr(out))
-    assert rc == 0
+    if use_ref:
+        r = ref()
+        lib.orc_set_conv_impl(C.cast(r.ref_conv_cpu, C.c_void_p), C.cast(r.ref_convT_cpu, C.c_void_p))
+    try:
+        C_, T = x.shape
+        out = np.zeros_like(x)
+        wa = (F * 18)(*[fptr(w) for w in wts])
+        ba = (F * 18)(*[fptr(b) for b in bts])
+        rc = lib.orc_mrf(wa, ba, C_, T, fptr(np.ascontiguousarray(x)), alpha, fptr(out))
+        assert rc == 0
+    finally:
+        if use_ref:
+            lib.orc_set_conv_impl(None, None)
     return out
 
 

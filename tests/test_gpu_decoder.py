@@ -201,6 +201,25 @@ def test_batched_decode_matches_single(env, T, batch):
     dz.free(); dw.free()
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,batch", [(226, 1), (97, 3)])
+def test_xcd_tile_order_same_result(env, T, batch, monkeypatch):
+    """The opt-in XCD-aware tile order (PTK_XCD_MAP=1) only permutes which workgroup computes
+    which tile: the waveform is bit-identical to the plain order's."""
+    ctx, model, ws, bs = env
+    say(f"xcd tile order T={T} batch={batch}")
+    dz = dev_of(ctx, np.stack([synth.latent(T, 700 + i) for i in range(batch)]))
+    dw = pkg.DevBuf(batch * 256 * T)
+    outs = []
+    for flag in ("0", "1"):
+        monkeypatch.setenv("PTK_XCD_MAP", flag)
+        assert ctx.lib.ptd_decode(ctx.ptr, model.ptr, dz.ptr, T, batch, dw.ptr) == 0
+        outs.append(dw.download(ctx))
+    monkeypatch.delenv("PTK_XCD_MAP")
+    assert np.array_equal(outs[0], outs[1])
+    dz.free(); dw.free()
+
+
 def _oracle_windows(ws, bs, z, win, ctx_):
     """The reference's overlap-save schedule (main_v21_serve.c:229-257) composed on the oracle."""
     T = z.shape[-1]
