@@ -255,7 +255,7 @@ double pt_v21_cuda_weights_mib(pt_ctx *c) {
 /* ================================================================== arena */
 void *ptdi_arena_alloc(pt_ctx *c, size_t bytes) {
   const size_t off = (c->g_arena_used + 255) & ~(size_t) 255;
-  if (!c->g_arena || off + bytes > c->g_arena_bytes) return NULL;
+  if (!c->g_arena || off > c->g_arena_bytes || bytes > c->g_arena_bytes - off) return NULL;
   c->g_arena_used = off + bytes;
   if (c->g_arena_used > c->arena_alloc_bytes) c->arena_alloc_bytes = c->g_arena_used;
   return (char *) c->g_arena + off;
@@ -275,12 +275,16 @@ static volatile int g_n_active, g_n_waiting;
 
 void pt_v21_cuda_active(int delta) { __sync_add_and_fetch(&g_n_active, delta); }
 
+static int g_wait_us, g_wait_adapt;
+static pthread_once_t g_wait_once = PTHREAD_ONCE_INIT;
+static void wait_policy_read(void) {
+  g_wait_adapt = env_int("PT_V21_WAIT_ADAPT", 1);
+  g_wait_us = env_int("PT_V21_WAIT_US", 0);
+}
+
 int ptdi_wait(pt_ctx *c) {
-  static int wait_us = -1, adapt = 1;   /* read once; a benign race between first callers */
-  if (wait_us < 0) {
-    adapt = env_int("PT_V21_WAIT_ADAPT", 1);
-    wait_us = env_int("PT_V21_WAIT_US", 0);
-  }
+  pthread_once(&g_wait_once, wait_policy_read);
+  const int wait_us = g_wait_us, adapt = g_wait_adapt;
   if (wait_us <= 0) return ptk_stream_sync(c->g_stream);
   /* the default 50 us timer slack would stretch each short poll sleep (PT_V21_SLACK0 keeps it) */
   static __thread int slack_set;
@@ -354,6 +358,11 @@ int ptdi_ctx_init(pt_ctx *c, size_t arena_bytes, int verbose) {
   const int upload = P.setup;
   pthread_mutex_unlock(&P.lock);
   if (r == 0 && upload) r = pool_claim_upload(c);
+  if (r) {
+    /* leave nothing behind: stream, arena and the pool reference taken above */
+    pt_v21_cuda_shutdown(c);
+    return -1;
+  }
   c->dev_bytes_weights = (double) P.data_bytes;
   if (verbose)
     PT_LOG("context ready: %.1f MiB shared weights, %zu MiB arena",
