@@ -15,6 +15,8 @@ on this host on a bounded sample.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
        python bench.py --kernel-loop N   (only the dominant kernel and the tail kernel, N launches
                                           each: for rocprofv3 --pmc)
+       python bench.py --decode-loop N [--batch B]   (N config-4 decodes, for a kernel trace)
+       python bench.py --layer-table KERNEL_TRACE_CSV [--batch B]   (per-launch table of that trace)
 """
 from __future__ import annotations
 
@@ -117,6 +119,65 @@ def tail_bytes(L, batch):
     return 4.0 * batch * (72 * L + 16 * (L - 1))
 
 
+DECODE_LOOP_WARM = 3
+
+# The 19 launches of one decode at T = 226 frames, in issue order (pt_decoder.c decode_impl), with
+# the algorithmic work of one request: flop for the conv launches (the MRF entries are grouped
+# launches of the three branch convs, K 3 + 7 + 11), HBM bytes for the elementwise and tail ones.
+_T1, _T2, _L = 4 * 226, 16 * 226, 16 * 226 + 1
+DECODE_LAUNCHES = (
+    [("conv_pre 192->512 K7", "flop", 2.0 * 512 * 192 * 7 * 226),
+     ("ups.0 convT 512->256 K16 s4", "flop", 2.0 * 256 * 512 * 4 * _T1)]
+    + [(f"MRF-256 d{d} {w} (K 3/7/11)", "flop", 2.0 * 256 * 256 * _T1 * 21)
+       for d in (1, 3, 5) for w in ("c1", "c2")]
+    + [("branch avg + leaky (256)", "bytes", 4.0 * 4 * 256 * _T1),
+       ("ups.1 convT 256->128 K16 s4", "flop", 2.0 * 128 * 256 * 4 * _T2)]
+    + [(f"MRF-128 d{d} {w} (K 3/7/11)", "flop", 2.0 * 128 * 128 * _T2 * 21)
+       for d in (1, 3, 5) for w in ("c1", "c2")]
+    + [("branch avg + leaky (128)", "bytes", 4.0 * 4 * 128 * _T2),
+       ("conv_post 128->72 K7", "flop", 2.0 * 72 * 128 * 7 * _L),
+       ("tail: iSTFT + PQMF", "bytes", 4.0 * (72 * _L + 16 * (_L - 1)))])
+
+
+def layer_table(csv_path, batch):
+    """Per-launch table of `bench.py --decode-loop N --batch B` from a rocprofv3 kernel trace: the
+    decoder's dispatches (weight relayouts and copies excluded) in issue order, cut into decodes
+    of 19, the warm-up decodes dropped, each position averaged over the rest."""
+    import csv
+    rows = [r for r in csv.DictReader(open(csv_path)) if r.get("Kind", "KERNEL_DISPATCH") == "KERNEL_DISPATCH"]
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    keep = ("conv_mfma_kernel", "avg3_leaky_kernel", "tail_kernel")
+    ks = [r for r in rows if r["Kernel_Name"].removeprefix("void ").startswith(keep)]
+    n = len(DECODE_LAUNCHES)
+    if len(ks) % n:
+        raise SystemExit(f"{len(ks)} decoder dispatches is not a multiple of {n}")
+    dec = [ks[i:i + n] for i in range(0, len(ks), n)][DECODE_LOOP_WARM:]
+    out = [f"{len(dec)} decodes of T = 226 x batch {batch} (after {DECODE_LOOP_WARM} warm-up decodes)", "",
+           "| # | launch | kernel | us | rate | % of peak |", "|---|---|---|---|---|---|"]
+    tot_us = tot_flop = 0.0
+    for i, (name, kind, work) in enumerate(DECODE_LAUNCHES):
+        names = {d[i]["Kernel_Name"] for d in dec}
+        if len(names) != 1:
+            raise SystemExit(f"launch {i} is not one kernel across decodes: {names}")
+        us = sum(int(d[i]["End_Timestamp"]) - int(d[i]["Start_Timestamp"]) for d in dec) / len(dec) / 1e3
+        kname = names.pop().replace("void ", "").split("(")[0]
+        w = work * batch
+        tot_us += us
+        if kind == "flop":
+            tot_flop += w
+            rate = w / (us * 1e-6) / 1e12
+            out.append(f"| {i} | {name} | `{kname}` | {us:.2f} | {rate:.1f} TFLOP/s | "
+                       f"{100 * rate / MFMA_F32_PEAK:.1f} % fp32 MFMA |")
+        else:
+            rate = w / (us * 1e-6) / 1e9
+            out.append(f"| {i} | {name} | `{kname}` | {us:.2f} | {rate:.0f} GB/s | "
+                       f"{100 * rate / HBM_PEAK:.1f} % HBM |")
+    out += ["", f"sum of kernel times: {tot_us:.1f} us per decode; conv launches "
+                f"{tot_flop / 1e9:.2f} GFLOP = {tot_flop / (tot_us * 1e-6) / 1e12:.1f} TFLOP/s over "
+                f"the kernel time (gaps between launches excluded)"]
+    return "\n".join(out)
+
+
 def cpu_baseline(pkg):
     """The reference's own CPU conv path (oracle/_ref, built from the reference sources) inside the
     oracle's decoder driver, or the C restatement when _ref is absent.  Timed two ways: config 5's
@@ -203,7 +264,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-loop", type=int, default=0)
+    ap.add_argument("--decode-loop", type=int, default=0)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--layer-table", metavar="KERNEL_TRACE_CSV")
     args = ap.parse_args()
+    if args.layer_table:
+        print(layer_table(args.layer_table, args.batch))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the decoder path would shard by request, with no exchange between GPUs)", file=sys.stderr)
@@ -215,6 +282,18 @@ def main():
     ws, bs = pkg.synth.decoder_weights(1234)
     model = pkg.Model(ctx, ws, bs)
     timer = EventTimer(pkg, ctx)
+
+    if args.decode_loop:
+        # config 4 decodes (T = 226, `--batch` requests per decode), eager, for a kernel trace
+        B = args.batch
+        dz = pkg.DevBuf.of(ctx, np.stack([pkg.synth.latent(226, 226 + i) for i in range(B)]))
+        dw = pkg.DevBuf(B * HOP * 226)
+        for _ in range(DECODE_LOOP_WARM + args.decode_loop):
+            if lib.ptd_decode(ctx.ptr, model.ptr, dz.ptr, 226, B, dw.ptr) != 0:
+                raise RuntimeError("decode failed")
+        ctx.sync()
+        log(f"decode loop: {DECODE_LOOP_WARM} + {args.decode_loop} decodes of T 226 x {B} done")
+        return
 
     # ---------------------------------------------------------------- dominant kernel
     # one MRF-256 depth at config 3 (C=256, T=904): two grouped conv launches of 3 branches each
