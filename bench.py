@@ -557,7 +557,7 @@ def main():
         **cfg,
     }
     if not args.no_cpu_baseline:
-        log("cpu baseline (reference conv path: 8 pinned threads, then 1 thread) ...")
+        log("cpu baseline (reference conv path: 8 pinned threads, then 1 thread for config 4 and configs 1-3) ...")
         out["cpu_baseline"] = cpu_baseline(pkg)
     timer.close()
     model.close()
