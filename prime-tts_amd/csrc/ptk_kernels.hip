@@ -579,13 +579,8 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
     yb[yi] = val;
     if (y2b != nullptr) y2b[yi] = val >= 0.0f ? val : a2 * val;
   };
-  if (S == 1) {
-#pragma unroll
-    for (int nb = 0; nb < NB; nb++)
-#pragma unroll
-      for (int v = 0; v < 16; v++) emit(nb, v, acc[nb][v]);
-    return;
-  }
+  // S = 1 takes the same path (each wave reads its own block back): one rolled store loop keeps
+  // the kernel's code small
   __syncthreads();
   float *red = smem;
 #pragma unroll
