@@ -1,0 +1,92 @@
+"""bench.py's per-launch decode table (`--layer-table`), on a synthetic rocprofv3 kernel trace:
+dispatch order, the warm-up cut, per-position averages and the rates against the peaks."""
+from __future__ import annotations
+
+import csv
+import importlib.util
+import pathlib
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+
+
+def _bench():
+    spec = importlib.util.spec_from_file_location("bench_mod", ROOT / "bench.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def _kernel_of(name):
+    if name.startswith("branch avg"):
+        return "avg3_leaky_kernel(float const*, float const*, float const*, float*, long long, float)"
+    if name.startswith("tail"):
+        return "tail_kernel(float const*, long long, long long, long long, float*, long long)"
+    return "void conv_mfma_kernel<11, 1, 0>(ConvGroup)"
+
+
+def _write_trace(path, bench, ndec, us_of, extra_first=True):
+    cols = ["Kind", "Agent_Id", "Queue_Id", "Stream_Id", "Thread_Id", "Dispatch_Id", "Kernel_Id",
+            "Kernel_Name", "Correlation_Id", "Start_Timestamp", "End_Timestamp"]
+    rows, did, t = [], 1, 1_000_000
+    if extra_first:   # a weight relayout and an upload copy before the decodes: not decoder launches
+        for name in ("relayout_kernel(float*, float const*, int, int, int, int, long long)",
+                     "__amd_rocclr_copyBuffer"):
+            rows.append([name, t, t + 5000])
+            t += 10000
+    for dec in range(ndec):
+        for i, (name, _, _) in enumerate(bench.DECODE_LAUNCHES):
+            ns = int(us_of(dec, i) * 1000)
+            rows.append([_kernel_of(name), t, t + ns])
+            t += ns + 1500
+    # rows out of dispatch order in the file: the table must sort them
+    order = list(range(len(rows)))
+    order = order[1::2] + order[0::2]
+    with open(path, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(cols)
+        for k in order:
+            name, t0, t1 = rows[k]
+            w.writerow(["KERNEL_DISPATCH", "Agent 1", 1, 1, 7, k + 1, 3, name, k + 1, t0, t1])
+
+
+def test_layer_table_averages_after_warmup(tmp_path):
+    bench = _bench()
+    n = len(bench.DECODE_LAUNCHES)
+    assert n == 19
+    warm = bench.DECODE_LOOP_WARM
+
+    # warm-up decodes are 10x slower; measured decodes alternate 10 us / 30 us at position i
+    def us_of(dec, i):
+        base = 10.0 + i if dec % 2 == 0 else 30.0 + i
+        return 10 * base if dec < warm else base
+
+    p = tmp_path / "trace.csv"
+    _write_trace(p, bench, warm + 4, us_of)
+    text = bench.layer_table(str(p), 1)
+    lines = [ln for ln in text.splitlines() if ln.startswith("| ") and ln[2].isdigit()]
+    assert len(lines) == n
+    for i, ln in enumerate(lines):
+        cells = [c.strip() for c in ln.strip("|").split("|")]
+        assert int(cells[0]) == i
+        # decodes warm..warm+3 are even/odd alternately: mean of (10+i, 30+i) = 20+i
+        assert float(cells[3]) == pytest.approx(20.0 + i, abs=0.01)
+    # conv_pre: 311 MFLOP in 20 us
+    first = [c.strip() for c in lines[0].strip("|").split("|")]
+    assert first[4] == f"{2 * 512 * 192 * 7 * 226 / 20e-6 / 1e12:.1f} TFLOP/s"
+    assert "sum of kernel times" in text
+
+
+def test_layer_table_rejects_a_partial_decode(tmp_path):
+    bench = _bench()
+    p = tmp_path / "trace.csv"
+    _write_trace(p, bench, 5, lambda dec, i: 10.0)
+    with open(p) as f:
+        body = f.read().splitlines()
+    # drop one decoder dispatch: 5 * 19 - 1 is not a multiple of 19
+    victim = next(k for k, ln in enumerate(body) if "tail_kernel" in ln)
+    del body[victim]
+    p.write_text("\n".join(body) + "\n")
+    with pytest.raises(SystemExit):
+        bench.layer_table(str(p), 1)
