@@ -16,7 +16,9 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
        python bench.py --kernel-loop N   (only the dominant kernel and the tail kernel, N launches
                                           each: for rocprofv3 --pmc)
        python bench.py --decode-loop N [--batch B]   (N config-4 decodes, for a kernel trace)
-       python bench.py --layer-table KERNEL_TRACE_CSV [--batch B]   (per-launch table of that trace)
+       python bench.py --layer-table KERNEL_TRACE_CSV [--batch B] [--counters COUNTER_CSV]
+                                          (per-launch table of that trace, MFMA utilisation from a
+                                          --pmc pass over the same loop)
 """
 from __future__ import annotations
 
@@ -139,21 +141,49 @@ DECODE_LAUNCHES = (
        ("tail: iSTFT + PQMF", "bytes", 4.0 * (72 * _L + 16 * (_L - 1)))])
 
 
-def layer_table(csv_path, batch):
-    """Per-launch table of `bench.py --decode-loop N --batch B` from a rocprofv3 kernel trace: the
-    decoder's dispatches (weight relayouts and copies excluded) in issue order, cut into decodes
-    of 19, the warm-up decodes dropped, each position averaged over the rest."""
-    import csv
-    rows = [r for r in csv.DictReader(open(csv_path)) if r.get("Kind", "KERNEL_DISPATCH") == "KERNEL_DISPATCH"]
-    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
-    keep = ("conv_mfma_kernel", "avg3_leaky_kernel", "tail_kernel")
-    ks = [r for r in rows if r["Kernel_Name"].removeprefix("void ").startswith(keep)]
+_DECODER_KERNELS = ("conv_mfma_kernel", "avg3_leaky_kernel", "tail_kernel")
+GRBM_XCDS, SIMDS = 8, 1024     # GRBM_GUI_ACTIVE sums the 8 XCDs; 256 CUs x 4 SIMDs
+
+
+def _decodes(rows):
+    """Decoder dispatches (weight relayouts and copies excluded) in issue order, cut into decodes
+    of 19, the warm-up decodes dropped."""
+    rows = sorted(rows, key=lambda r: int(r["Dispatch_Id"]))
+    ks = [r for r in rows if r["Kernel_Name"].removeprefix("void ").startswith(_DECODER_KERNELS)]
     n = len(DECODE_LAUNCHES)
     if len(ks) % n:
         raise SystemExit(f"{len(ks)} decoder dispatches is not a multiple of {n}")
-    dec = [ks[i:i + n] for i in range(0, len(ks), n)][DECODE_LOOP_WARM:]
+    return [ks[i:i + n] for i in range(0, len(ks), n)][DECODE_LOOP_WARM:]
+
+
+def _mfma_util(counter_csv):
+    """Per launch position: mean MFMA utilisation, SQ_VALU_MFMA_BUSY_CYCLES /
+    (GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs) (rocprofv3's MfmaUtil), from a --pmc pass over the
+    same decode loop."""
+    import csv
+    by = {}
+    for r in csv.DictReader(open(counter_csv)):
+        e = by.setdefault(r["Dispatch_Id"], {"Dispatch_Id": r["Dispatch_Id"], "Kernel_Name": r["Kernel_Name"]})
+        e[r["Counter_Name"]] = float(r["Counter_Value"])
+    dec = _decodes(list(by.values()))
+    out = []
+    for i in range(len(DECODE_LAUNCHES)):
+        u = [d[i]["SQ_VALU_MFMA_BUSY_CYCLES"] / (d[i]["GRBM_GUI_ACTIVE"] / GRBM_XCDS * SIMDS) for d in dec]
+        out.append(100.0 * sum(u) / len(u))
+    return out
+
+
+def layer_table(csv_path, batch, counter_csv=None):
+    """Per-launch table of `bench.py --decode-loop N --batch B` from a rocprofv3 kernel trace, each
+    launch position averaged over the decodes after the warm-up; with a --pmc pass of
+    SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE over the same loop, the MFMA utilisation too."""
+    import csv
+    rows = [r for r in csv.DictReader(open(csv_path)) if r.get("Kind", "KERNEL_DISPATCH") == "KERNEL_DISPATCH"]
+    dec = _decodes(rows)
+    util = _mfma_util(counter_csv) if counter_csv else None
+    head = "| # | launch | kernel | us | rate | % of peak |" + (" MFMA util % |" if util else "")
     out = [f"{len(dec)} decodes of T = 226 x batch {batch} (after {DECODE_LOOP_WARM} warm-up decodes)", "",
-           "| # | launch | kernel | us | rate | % of peak |", "|---|---|---|---|---|---|"]
+           head, "|---" * (7 if util else 6) + "|"]
     tot_us = tot_flop = 0.0
     for i, (name, kind, work) in enumerate(DECODE_LAUNCHES):
         names = {d[i]["Kernel_Name"] for d in dec}
@@ -167,11 +197,12 @@ def layer_table(csv_path, batch):
             tot_flop += w
             rate = w / (us * 1e-6) / 1e12
             out.append(f"| {i} | {name} | `{kname}` | {us:.2f} | {rate:.1f} TFLOP/s | "
-                       f"{100 * rate / MFMA_F32_PEAK:.1f} % fp32 MFMA |")
+                       f"{100 * rate / MFMA_F32_PEAK:.1f} % fp32 MFMA |"
+                       + (f" {util[i]:.1f} |" if util else ""))
         else:
             rate = w / (us * 1e-6) / 1e9
             out.append(f"| {i} | {name} | `{kname}` | {us:.2f} | {rate:.0f} GB/s | "
-                       f"{100 * rate / HBM_PEAK:.1f} % HBM |")
+                       f"{100 * rate / HBM_PEAK:.1f} % HBM |" + (" - |" if util else ""))
     out += ["", f"sum of kernel times: {tot_us:.1f} us per decode; conv launches "
                 f"{tot_flop / 1e9:.2f} GFLOP = {tot_flop / (tot_us * 1e-6) / 1e12:.1f} TFLOP/s over "
                 f"the kernel time (gaps between launches excluded)"]
@@ -267,9 +298,10 @@ def main():
     ap.add_argument("--decode-loop", type=int, default=0)
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--layer-table", metavar="KERNEL_TRACE_CSV")
+    ap.add_argument("--counters", metavar="COUNTER_COLLECTION_CSV")
     args = ap.parse_args()
     if args.layer_table:
-        print(layer_table(args.layer_table, args.batch))
+        print(layer_table(args.layer_table, args.batch, args.counters))
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "

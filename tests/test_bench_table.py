@@ -90,3 +90,38 @@ def test_layer_table_rejects_a_partial_decode(tmp_path):
     p.write_text("\n".join(body) + "\n")
     with pytest.raises(SystemExit):
         bench.layer_table(str(p), 1)
+
+
+def test_layer_table_mfma_util_from_counters(tmp_path):
+    """--counters: per launch position, SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 x 1024)
+    averaged over the measured decodes; '-' for the launches without MFMA work."""
+    bench = _bench()
+    warm = bench.DECODE_LOOP_WARM
+    trace = tmp_path / "trace.csv"
+    _write_trace(trace, bench, warm + 2, lambda dec, i: 10.0)
+    cols = ["Correlation_Id", "Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"]
+    rows, did = [], 1
+    rows.append([did, did, "relayout_kernel(float*)", "GRBM_GUI_ACTIVE", 1.0])
+    rows.append([did, did, "relayout_kernel(float*)", "SQ_VALU_MFMA_BUSY_CYCLES", 0.0])
+    for dec in range(warm + 2):
+        for i, (name, _, _) in enumerate(bench.DECODE_LAUNCHES):
+            did += 1
+            gui = 8000.0                       # per SIMD: 8000 / 8 = 1000 cycles
+            frac = 0.9 if dec < warm else (0.2 + 0.01 * i if dec % 2 else 0.4 + 0.01 * i)
+            rows.append([did, did, _kernel_of(name), "GRBM_GUI_ACTIVE", gui])
+            rows.append([did, did, _kernel_of(name), "SQ_VALU_MFMA_BUSY_CYCLES", frac * 1000 * 1024])
+    pmc = tmp_path / "pmc.csv"
+    with open(pmc, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(cols)
+        w.writerows(rows)
+    text = bench.layer_table(str(trace), 1, str(pmc))
+    lines = [ln for ln in text.splitlines() if ln.startswith("| ") and ln[2].isdigit()]
+    assert len(lines) == len(bench.DECODE_LAUNCHES)
+    for i, ln in enumerate(lines):
+        cells = [c.strip() for c in ln.strip("|").split("|")]
+        kind = bench.DECODE_LAUNCHES[i][1]
+        if kind == "flop":
+            assert float(cells[6]) == pytest.approx(100 * (0.3 + 0.01 * i), abs=0.05)
+        else:
+            assert cells[6] == "-"
