@@ -234,6 +234,7 @@ def cpu_baseline(pkg):
     dt1 = time.perf_counter() - t0
     audio1 = T * HOP / SR
     layers = _cpu_layers(pkg, ol, ws, bs, use_ref, cores[0])
+    mm = _cpu_matmul(ol) if use_ref else None
     return {"value": round(audio8 / dt8, 4), "unit": "audio-s/s", "cores": nthr, "kind": kind,
             "sample": f"config 5's 8 requests (T={Ts}, {audio8:.2f} s audio; the T=1500 long-form "
                       f"request not included) as {nthr} threads pinned to cores {cores[:nthr]}: "
@@ -242,7 +243,28 @@ def cpu_baseline(pkg):
                               "sample": f"one config-4 decode (T=226, {audio1:.3f} s audio) on 1 "
                                         f"thread: {dt1:.2f} s"},
             "configs_1_3_single_thread": layers,
+            "matmul_us_per_call": mm,
             "host_cpus": len(cores), "nproc": os.cpu_count(), "model": _cpu_model()}
+
+
+MATMUL_SHAPES = [(37, 53, 29), (120, 192, 120), (120, 96, 192)]   # m, k, n: encoder attention
+
+
+def _cpu_matmul(ol):
+    """The reference's CPU matmul (pt_v21_matmul_cpu) at the shapes the device matmul is timed on,
+    on the calling thread: us per call."""
+    out = {}
+    for m_, k_, n_ in MATMUL_SHAPES:
+        rngm = np.random.default_rng(m_ + k_ + n_)
+        A = rngm.standard_normal((m_, k_)).astype(np.float32)
+        B = rngm.standard_normal((k_, n_)).astype(np.float32)
+        Cm = np.zeros((m_, n_), np.float32)
+        ol.ref_matmul(A, m_, k_, k_, B, n_, n_, Cm, n_)
+        t0 = time.perf_counter()
+        for _ in range(50):
+            ol.ref_matmul(A, m_, k_, k_, B, n_, n_, Cm, n_)
+        out[f"{m_}x{k_}x{n_}"] = round((time.perf_counter() - t0) / 50 * 1e6, 1)
+    return out
 
 
 def _cpu_layers(pkg, ol, ws, bs, use_ref, core):
@@ -466,7 +488,7 @@ def main():
                  "total_ms": round((t2 - t0) * 1e3, 2)}
     log(f"container load: {container}")
     mm = {}
-    for m_, k_, n_ in [(37, 53, 29), (120, 192, 120), (120, 96, 192)]:
+    for m_, k_, n_ in MATMUL_SHAPES:
         rngm = np.random.default_rng(m_ + k_ + n_)
         A = rngm.standard_normal((m_, k_)).astype(np.float32)
         B = rngm.standard_normal((k_, n_)).astype(np.float32)

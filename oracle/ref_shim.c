@@ -2,7 +2,8 @@
  * runtime/v21/src/pt_v21_host.c and runtime/v21/gen/pt_graph.c (unmodified, where they lie) into
  * oracle/_ref/libptref.so.  It gives the reference's CPU conv path a context-free entry point with
  * the oracle's signatures, so tests can check the C restatement against the reference's own code
- * and bench.py can time that code as the CPU baseline.  It also reports the reference's struct
+ * and bench.py can time that code as the CPU baseline (the CPU matmul likewise, for the device
+ * matmul's tests and baseline).  It also reports the reference's struct
  * pt_ctx layout, which the HIP library's own declaration must match field for field. */
 #include <stddef.h>
 #include <stdlib.h>
@@ -25,6 +26,13 @@ int ref_convT_cpu(const float *X, int64_t ldx, int64_t cin, int64_t tin, float *
   pt_ctx c;
   memset(&c, 0, sizeof c);
   return pt_v21_convT_cpu(&c, X, ldx, cin, tin, Y, ldy, cout, s, pad, K, wp, bias, batch, -1, -1);
+}
+
+int ref_matmul_cpu(const float *A, int64_t m, int64_t k, int64_t lda, const float *B, int64_t ldb,
+                   int64_t n, float *C, int64_t ldc) {
+  pt_ctx c;
+  memset(&c, 0, sizeof c);
+  return pt_v21_matmul_cpu(&c, A, m, k, lda, B, ldb, n, C, ldc);
 }
 
 /* sizeof(pt_ctx) followed by the offsets of the fields the device layer reads or writes */

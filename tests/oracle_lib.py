@@ -60,8 +60,15 @@ def ref():
         lib.ref_conv_cpu.argtypes = CONV_ARGS
         lib.ref_convT_cpu.argtypes = CONVT_ARGS
         lib.ref_ctx_layout.argtypes = [C.POINTER(C.c_long), C.c_int]
+        lib.ref_matmul_cpu.argtypes = [F, I64, I64, I64, F, I64, I64, F, I64]
         _ref = lib
     return _ref
+
+
+def ref_matmul(A, m, k, lda, B, ldb, n, Cm, ldc):
+    """The reference's CPU matmul (pt_v21_matmul_cpu, pt_v21_host.c:2635-2650) in place on Cm."""
+    assert ref().ref_matmul_cpu(fptr(A), m, k, lda, fptr(B), ldb, n, fptr(Cm), ldc) == 0
+    return Cm
 
 
 def pad_rows(x: np.ndarray, pad: int) -> np.ndarray:

@@ -278,6 +278,15 @@ def test_matmul(ctx, m, k, n, pad):
     else:
         assert relerr(Cf[:, :n], ref) < 1e-5
     assert np.all(Cf[:, n:] == 7.0)   # columns past n untouched
+    if ol.have_ref():
+        # the reference's own CPU matmul on the same operands: same values within fp32 summation
+        # order, and the same untouched padding
+        Cr = ol.ref_matmul(Af, m, k, lda, Bf, ldb, n, np.full((m, ldc), 7.0, np.float32), ldc)
+        if k == 0:
+            assert np.array_equal(Cr, Cf)
+        else:
+            assert relerr(Cf[:, :n], Cr[:, :n].astype(np.float64)) < 1e-5
+        assert np.all(Cr[:, n:] == 7.0)
 
 
 def test_device_residency(ctx):

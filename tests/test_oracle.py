@@ -259,6 +259,24 @@ def test_decoder_ref_conv_bitexact():
     assert np.array_equal(ol.decoder(ws, bs, z), ol.decoder(ws, bs, z, use_ref=True))
 
 
+@pytest.mark.parametrize("m,k,n,pad", [(37, 53, 29, 0), (120, 96, 192, 3), (5, 0, 7, 2)])
+def test_ref_matmul_shim(m, k, n, pad):
+    """The reference's CPU matmul through the shim (the device matmul's second check and its CPU
+    baseline): C = A B over the first k / n columns, padding columns of C left as they were, and
+    k = 0 gives zeros."""
+    if not ol.have_ref():
+        pytest.skip("oracle/_ref not built (the reference tree is absent on this machine)")
+    rng = np.random.default_rng(m + n)
+    lda, ldb, ldc = k + pad, n + pad, n + pad
+    A = rng.standard_normal((m, max(lda, 1))).astype(np.float32)
+    B = rng.standard_normal((max(k, 1), ldb)).astype(np.float32)
+    Cm = np.full((m, ldc), 7.0, np.float32)
+    ol.ref_matmul(A, m, k, lda, B, ldb, n, Cm, ldc)
+    want = A[:, :k].astype(np.float64) @ B[:k, :n]
+    assert np.abs(Cm[:, :n] - want).max() <= 1e-5 * max(1.0, np.abs(want).max())
+    assert np.all(Cm[:, n:] == 7.0)
+
+
 def test_decoder_mutation_caught():
     """Dropping the /3 of the branch average (a plausible glue mistake) fails the float64 gate."""
     ws, bs, raw = synth.decoder_weights(7, raw=True)
