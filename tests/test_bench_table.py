@@ -125,3 +125,14 @@ def test_layer_table_mfma_util_from_counters(tmp_path):
             assert float(cells[6]) == pytest.approx(100 * (0.3 + 0.01 * i), abs=0.05)
         else:
             assert cells[6] == "-"
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """This build measures one GPU: --gpus N > 1 exits with a message before touching a device."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
+    assert r.stdout == ""
