@@ -209,11 +209,21 @@ def layer_table(csv_path, batch, counter_csv=None):
     return "\n".join(out)
 
 
-def cpu_baseline(pkg):
+def sndr_db(est, ref):
+    """Signal to noise-and-distortion ratio of est against ref, in dB."""
+    est = np.asarray(est, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = float(np.sum((est - ref) ** 2))
+    return float("inf") if err == 0.0 else float(10.0 * np.log10(float(np.sum(ref ** 2)) / err))
+
+
+def cpu_baseline(pkg, gpu_wavs=None):
     """The reference's own CPU conv path (oracle/_ref, built from the reference sources) inside the
     oracle's decoder driver, or the C restatement when _ref is absent.  Timed two ways: config 5's
     eight requests as eight host threads pinned to eight distinct cores (the reference's
-    one-thread-per-stream model, main_v21_par.c:134-140), and one config-4 request on one thread."""
+    one-thread-per-stream model, main_v21_par.c:134-140), and one config-4 request on one thread.
+    gpu_wavs: the same eight requests' waveforms from the timed GPU step, compared (SNDR) with the
+    CPU ones."""
     sys.path.insert(0, str(ROOT / "tests"))
     import oracle_lib as ol
     ws, bs = pkg.synth.decoder_weights(1234)
@@ -224,7 +234,7 @@ def cpu_baseline(pkg):
     Ts = pkg.synth.request_lengths(5, 8)
     zs = [pkg.synth.latent(T, 900 + i) for i, T in enumerate(Ts)]
     nthr = min(8, len(cores))
-    _, dt8 = ol.decoder_threads(ws, bs, zs, cores[:nthr], use_ref=use_ref)
+    cpu_wavs, dt8 = ol.decoder_threads(ws, bs, zs, cores[:nthr], use_ref=use_ref)
     audio8 = sum(Ts) * HOP / SR
     # one config-4 request on one thread
     T = 226
@@ -244,7 +254,10 @@ def cpu_baseline(pkg):
                                         f"thread: {dt1:.2f} s"},
             "configs_1_3_single_thread": layers,
             "matmul_us_per_call": mm,
-            "host_cpus": len(cores), "nproc": os.cpu_count(), "model": _cpu_model()}
+            "host_cpus": len(cores), "nproc": os.cpu_count(), "model": _cpu_model(),
+            # the same requests' waveforms from the timed GPU step against these CPU ones
+            "sndr_vs_gpu_db": [round(sndr_db(g, c), 2) for g, c in zip(gpu_wavs, cpu_wavs)]
+            if gpu_wavs is not None else None}
 
 
 MATMUL_SHAPES = [(37, 53, 29), (120, 192, 120), (120, 96, 192)]   # m, k, n: encoder attention
@@ -565,10 +578,20 @@ def main():
     audio_step = sum(Ts + [T_long]) * HOP / SR
     value = audio_step * args.steps / dt
     audio8 = sum(Ts) * HOP / SR
+    log(f"config 5: {value:.1f} audio-s/s ({dt / args.steps * 1e3:.2f} ms/step)")
+    # the timed step's own outputs (after the timed region): the eight requests are compared with
+    # the reference's CPU path in the cpu_baseline leg, the long-form windows with one full
+    # (unwindowed) decode of the same latents
+    c5_wavs = [b.download(ctx) for b in wv]
+    dfull = pkg.DevBuf(HOP * T_long)
+    if lib.ptd_decode(ctx.ptr, model.ptr, zs[-1].ptr, T_long, 1, dfull.ptr) != 0:
+        raise RuntimeError("full long-form decode failed")
+    parity = {"gate_db": 60.0,
+              "config5_longform_windows_vs_full_decode_sndr_db": round(sndr_db(c5_wavs[-1], dfull.download(ctx)), 2)}
+    dfull.free()
     lib.ptd_server_destroy(srv)
     for b in zs + wv:
         b.free()
-    log(f"config 5: {value:.1f} audio-s/s ({dt / args.steps * 1e3:.2f} ms/step)")
 
     out = {
         "metric": "decoder audio-sec/sec at 8 streams (+ conv TFLOP/s, % fp32-MFMA peak)",
@@ -610,9 +633,13 @@ def main():
         "matmul_us_per_call": mm,
         **cfg,
     }
+    out["parity"] = parity
     if not args.no_cpu_baseline:
         log("cpu baseline (reference conv path: 8 pinned threads, then 1 thread for config 4 and configs 1-3) ...")
-        out["cpu_baseline"] = cpu_baseline(pkg)
+        out["cpu_baseline"] = cpu_baseline(pkg, c5_wavs[:8])
+        snd = out["cpu_baseline"].pop("sndr_vs_gpu_db")
+        parity["config5_requests_vs_reference_cpu_sndr_db"] = {"min": min(snd), "per_request": snd}
+    log(f"parity: {parity}")
     timer.close()
     model.close()
     ctx.close()
