@@ -410,6 +410,18 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   // the wave-based buffer resources would be treated as divergent)
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ks = w % S, cg = w / S;             // channel split index, column group
+  // The block's 32 bias values go to LDS once, past the staging / reduction area, so that the
+  // epilogue adds them from LDS: a global load per element there, placed after the previous
+  // element's stores, would wait out a whole memory latency each time.
+  constexpr int BIAS_LDS = (CONV_WAVES * CONV_CK * XWMAX > CONV_WAVES * NB * 16 * 64)
+                               ? CONV_WAVES * CONV_CK * XWMAX : CONV_WAVES * NB * 16 * 64;
+  float *bsh = smem + BIAS_LDS;
+  if (w == 0 && lane < 32) {
+    const int m = mb * 32 + lane;
+    int co = m;
+    if (d.C4 != d.M) co = m - (m / d.C4) * d.C4;
+    bsh[lane] = (d.bias != nullptr && m < d.M && co < d.nbias) ? d.bias[co] : 0.0f;
+  }
   const int half = lane >> 5;     // which of the two reduction rows this lane feeds
   const int l32 = lane & 31;
   const long long q0 = d.q0 + ((long long) tn * G + cg) * (32 * NB);
@@ -555,9 +567,8 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   // epilogue: the S partial sums of a block are added in wave order through LDS, then bias, the
   // epilogue chain and one store per output
   const long long qend = d.q0 + d.nq;
-  const int M = d.M, C4 = d.C4, ys = d.ys, ypad = d.ypad, nbias = d.nbias, nepi = d.nepi;
+  const int M = d.M, C4 = d.C4, ys = d.ys, ypad = d.ypad, nepi = d.nepi;
   const long long Lout = d.Lout, ldy = d.ldy;
-  const float *bias = d.bias;
   float *yb = d.y + (long long) b * d.bsy;
   float *y2b = d.y2 != nullptr ? d.y2 + (long long) b * d.bsy : nullptr;
   const float a2 = d.a2;
@@ -573,7 +584,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
     }
     const long long col = q * ys + r - ypad;
     if (col < 0 || col >= Lout) return;
-    float val = sum + ((bias != nullptr && co < nbias) ? bias[co] : 0.0f);
+    float val = sum + bsh[m - mb * 32];
     for (int e = 0; e < nepi; e++) val = epi_apply(val, d.epi[e], b, co, col);
     const long long yi = (long long) co * ldy + col;
     yb[yi] = val;
@@ -789,7 +800,7 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
   if (total == 0) return 0;
   const size_t stage = (size_t) CONV_WAVES * CONV_CK * win_max(nb) * sizeof(float);
   const size_t redb = (size_t) CONV_WAVES * 16 * nb * 64 * sizeof(float);
-  const size_t lds = stage > redb ? stage : redb;
+  const size_t lds = (stage > redb ? stage : redb) + 32 * sizeof(float);   // + the block's bias
   hipStream_t s = (hipStream_t) stream;
   if (nb == 2) launch_conv_in<2>(in_op, kmax, g, total, lds, s);
   else launch_conv_in<1>(in_op, kmax, g, total, lds, s);
