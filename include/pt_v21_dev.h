@@ -129,7 +129,7 @@ int pt_v21_convT(pt_ctx *c, const float *X, int64_t ldx, int64_t cin, int64_t ti
                  int64_t ldy, int cout, int s, int pad, int K, const float *wp, const float *bias,
                  int64_t batch, int wtab, int btab);
 /* pt_v21.h:258 -- C[m][nn] = A[m][k] @ B[k][nn] on the device (encoder attention; off the hot
- * path, a plain SIMT kernel). */
+ * path): fp32 MFMA, 64x64 blocks of C, 32x32 per wave; host buffers, synchronous.  0 / -1. */
 int pt_v21_matmul(pt_ctx *c, const float *A, int64_t m, int64_t k, int64_t lda, const float *B,
                   int64_t ldb, int64_t nn, float *C, int64_t ldc);
 

@@ -133,7 +133,7 @@ def convT_weights(rng: np.random.Generator, cin: int, cout: int, K: int, s: int)
 def pqmf_synthesis() -> np.ndarray:
     """The model's PQMF synthesis filter, /dec/Constant_134 (1, 4, 63): the weight of the
     decoder's last conv (data/v21_pqmf_synthesis.npy, decoded from the reference's
-    spec/v21_layers.json by data/extract_constants.py)."""
+    spec/v21_layers.json by tests/golden/extract_constants.py)."""
     h = np.load(PQMF_FILE, allow_pickle=False)
     assert h.shape == (1, 4, 63) and h.dtype == np.float32
     return h

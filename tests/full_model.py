@@ -76,6 +76,23 @@ def write_container(path, seed: int = 0) -> None:
     pw.write(path, tensors(seed))
 
 
+def decoder_layers(seed: int = 0):
+    """The 41 decoder layers (synth.dec_layer order) of the container write_container(seed)
+    writes, as any reader of it sees them: packed weights with fp16 records expanded to fp32,
+    biases cut to cout.  Returns (ws, bs)."""
+    recs = {name: (a, isz) for name, a, isz in tensors(seed)}
+    ws, bs = [], []
+    for i in range(synth.N_LAYER):
+        mod = synth.layer_module(i)
+        a, isz = recs[mod + ".wp#h"] if mod + ".wp#h" in recs else recs[mod + ".wp"]
+        if isz == 2:
+            a = a.astype(np.float16).astype(np.float32)
+        ws.append(np.ascontiguousarray(a, np.float32))
+        b, _ = recs[mod + ".b"]
+        bs.append(np.ascontiguousarray(b[:synth.dec_layer(i)["cout"]], np.float32))
+    return ws, bs
+
+
 def write_case(case_dir, n_tokens: int = 40, seed: int = 0, sid: int = 0) -> None:
     """The seven graph feeds of one request (ids interleaved with blanks, as add_blank does) and a
     one-sample placeholder wav.npy for the driver's parity print."""

@@ -1,8 +1,8 @@
-"""Writes v21_pqmf_synthesis.npy: the MB-iSTFT decoder's PQMF synthesis filter, the model constant
+"""Writes prime-tts_amd/data/v21_pqmf_synthesis.npy: the MB-iSTFT decoder's PQMF synthesis filter, the model constant
 /dec/Constant_134 of shape (1, 4, 63) (the weight of the final /dec/Conv, 4 subbands -> 1 sample
 stream, 63 taps).  The reference keeps its raw fp32 bytes in spec/v21_layers.json (the node's
 "value" attribute, protobuf text format); this script decodes them.  Run where the reference tree
-exists: python prime-tts_amd/data/extract_constants.py [/root/reference]"""
+exists: python tests/golden/extract_constants.py [/root/reference]"""
 from __future__ import annotations
 
 import json
@@ -13,6 +13,7 @@ import sys
 import numpy as np
 
 HERE = pathlib.Path(__file__).resolve().parent
+DATA = HERE.parents[1] / "prime-tts_amd" / "data"
 ESC = {"n": 10, "t": 9, "r": 13, '"': 34, "'": 39, "\\": 92, "a": 7, "b": 8, "f": 12, "v": 11}
 
 
@@ -56,8 +57,8 @@ def main():
     spec = json.loads((ref / "spec" / "v21_layers.json").read_text())
     h = constant(spec, "/dec/Constant_134")
     assert h.shape == (1, 4, 63), h.shape
-    np.save(HERE / "v21_pqmf_synthesis.npy", h.astype(np.float32))
-    print(f"wrote {HERE / 'v21_pqmf_synthesis.npy'}: {h.shape}, band sums {h[0].sum(axis=1)}")
+    np.save(DATA / "v21_pqmf_synthesis.npy", h.astype(np.float32))
+    print(f"wrote {DATA / 'v21_pqmf_synthesis.npy'}: {h.shape}, band sums {h[0].sum(axis=1)}")
 
 
 if __name__ == "__main__":

@@ -21,7 +21,7 @@ import numpy as np
 
 HERE = pathlib.Path(__file__).resolve().parent
 _spec = importlib.util.spec_from_file_location(
-    "extract_constants", HERE.parents[1] / "prime-tts_amd" / "data" / "extract_constants.py")
+    "extract_constants", HERE / "extract_constants.py")
 extract = importlib.util.module_from_spec(_spec)
 _spec.loader.exec_module(extract)
 

@@ -227,7 +227,7 @@ def test_pqmf_filter_is_the_models():
     spec_file = pathlib.Path("/root/reference/spec/v21_layers.json")
     if spec_file.exists():
         import importlib.util
-        ex = ROOT / "prime-tts_amd" / "data" / "extract_constants.py"
+        ex = ROOT / "tests" / "golden" / "extract_constants.py"
         sp = importlib.util.spec_from_file_location("extract_constants", ex)
         mod = importlib.util.module_from_spec(sp)
         sp.loader.exec_module(mod)
