@@ -83,6 +83,16 @@ void ptd_model_destroy(ptd_model *m);
 int ptd_decode(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int batch, float *wav);
 /* arena bytes one ptd_decode call needs */
 size_t ptd_decode_arena_bytes(int64_t T, int batch);
+/* No counterpart in the reference.  For callers that cannot allocate device memory (code under
+ * HIP stream capture, serving loops that forbid hipMalloc): ptd_decode with its activations in a
+ * static device scratch of the library (64 MiB per GPU, held until the process ends) instead of
+ * the context's arena.  It allocates nothing.  A decode needing more than the scratch
+ * (ptd_decode_arena_bytes(T, batch) > 64 MiB, e.g. batch 1 above 435 frames) is refused: -1 and a
+ * stderr line, nothing queued.  Every call on one GPU shares that GPU's scratch: calls that
+ * overlap in time on one GPU (other contexts' streams) race and must be serialised by the caller;
+ * calls on one stream are ordered.  Same output bits as ptd_decode.  Asynchronous.  0 / -1. */
+int ptd_decode_noalloc(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int batch,
+                       float *wav);
 /* Same, also copying the six stage tensors (conv_pre+leaky, ups.0, MRF-256 out, ups.1, MRF-128
  * out, conv_post) of batch item 0 into the given device buffers (entries may be NULL). */
 int ptd_decode_stages(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, float *wav,

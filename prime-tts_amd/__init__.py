@@ -63,6 +63,7 @@ _SIGS = {
     "ptd_model_create": (VP, [VP, C.POINTER(F), C.POINTER(F)]),
     "ptd_model_destroy": (None, [VP]),
     "ptd_decode": (C.c_int, [VP, VP, VP, I64, C.c_int, VP]),
+    "ptd_decode_noalloc": (C.c_int, [VP, VP, VP, I64, C.c_int, VP]),
     "ptd_decode_arena_bytes": (C.c_size_t, [I64, C.c_int]),
     "ptd_decode_stages": (C.c_int, [VP, VP, VP, I64, VP, C.POINTER(VP)]),
     "ptd_layer": (C.c_int, [VP, VP, C.c_int, VP, I64, C.c_int, VP, C.c_float, C.c_float]),

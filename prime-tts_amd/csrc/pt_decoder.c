@@ -385,6 +385,41 @@ int ptd_decode(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int bat
   return decode_impl(c, m, z, T, 192 * T, T, batch, wav, 256 * T, NULL, NULL);
 }
 
+/* ptd_decode with its activations in the library's static device scratch instead of the
+ * context's arena: nothing is allocated, so a caller that may not allocate device memory (inside
+ * a stream capture, a serving loop that forbids it) can decode.  The scratch is shared by every
+ * call on the GPU and keeps the last call's contents; every activation is written before it is
+ * read, so nothing needs clearing. */
+int ptd_decode_noalloc(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int batch,
+                       float *wav) {
+  if (!c || !c->use_cuda || !m || !z || !wav || T < 1 || batch < 1) return -1;
+  void *base = NULL;
+  size_t cap = 0;
+  if (ptk_static_scratch(&base, &cap)) {
+    PT_LOG("ptd_decode_noalloc: %s", ptk_last_error());
+    return -1;
+  }
+  /* T * batch bounded first, so the size below cannot overflow */
+  const size_t need = T > ((int64_t) 1 << 32) / batch ? (size_t) -1 : ptd_decode_arena_bytes(T, batch);
+  if (need > cap) {
+    PT_LOG("ptd_decode_noalloc: a decode of T %lld x %d needs %zu MiB of scratch; the static "
+           "scratch holds %zu MiB", (long long) T, batch, need == (size_t) -1 ? need : need >> 20,
+           cap >> 20);
+    return -1;
+  }
+  void *a0 = c->g_arena;
+  const size_t b0 = c->g_arena_bytes, u0 = c->g_arena_used, h0 = c->arena_alloc_bytes;
+  c->g_arena = base;
+  c->g_arena_bytes = cap;
+  c->g_arena_used = 0;
+  const int rc = ptd_decode(c, m, z, T, batch, wav);
+  c->g_arena = a0;
+  c->g_arena_bytes = b0;
+  c->g_arena_used = u0;
+  c->arena_alloc_bytes = h0;
+  return rc;
+}
+
 int ptd_decode_stages(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, float *wav,
                       float *const *stages) {
   return decode_impl(c, m, z, T, 192 * T, T, 1, wav, 256 * T, NULL, stages);

@@ -47,6 +47,10 @@ int ptk_capture_begin(void *s);
 int ptk_capture_end(void *s, void **exec);
 int ptk_graph_launch(void *exec, void *s);
 int ptk_graph_destroy(void *exec);
+/* The library's static device scratch (no allocation): the current device's copy, its address
+ * resolved once per device at ptk_init.  All users of one GPU share it.  0 / -1. */
+#define PTK_STATIC_SCRATCH_BYTES ((size_t) 64 << 20)
+int ptk_static_scratch(void **p, size_t *bytes);
 
 /* ---------------------------------------------------------------- conv problem descriptor
  * One implicit-GEMM problem.  Row m of the GEMM is an output channel (conv: m = co) or a phase

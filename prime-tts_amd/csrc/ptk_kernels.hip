@@ -46,6 +46,47 @@ static void set_err(const char *fmt, ...) {
 
 extern "C" const char *ptk_last_error(void) { return g_err; }
 
+// ------------------------------------------------------------------------------ static scratch
+// Device memory for callers that cannot allocate any (ptd_decode_noalloc): one array per GPU,
+// loaded with the code object and held until the process ends.  On the host, `scratch` is only a
+// stand-in for the symbol; host code uses the device address hipGetSymbolAddress gives for the
+// current device (each GPU has its own copy at its own address), kept per device below.  Every
+// user of a GPU shares that GPU's array: work that overlaps in time on one GPU races on it.
+static __device__ __align__(256) unsigned char scratch[PTK_STATIC_SCRATCH_BYTES];
+#define PTK_SCRATCH_MAX_DEVICES 64
+static std::mutex g_scratch_lock;
+static void *g_scratch_ptr[PTK_SCRATCH_MAX_DEVICES];
+
+// resolve (once per device) the current device's copy of `scratch`
+static int scratch_resolve(void **out) {
+  int dev = -1;
+  HCHK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= PTK_SCRATCH_MAX_DEVICES) {
+    set_err("static scratch: device %d out of range", dev);
+    return -1;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_lock);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    HCHK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) {
+      set_err("static scratch: hipGetSymbolAddress gave NULL on device %d", dev);
+      return -1;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+extern "C" int ptk_static_scratch(void **p, size_t *bytes) {
+  *p = nullptr;
+  *bytes = 0;
+  if (scratch_resolve(p)) return -1;
+  *bytes = PTK_STATIC_SCRATCH_BYTES;
+  return 0;
+}
+
 // ------------------------------------------------------------------------------ runtime wrappers
 // Device 0 for the calling thread.  The device count is queried once per process; the current
 // device is per-thread HIP state, so every thread that creates a context selects it itself (the
@@ -64,6 +105,10 @@ extern "C" int ptk_init(void) {
   if (!selected) {
     HCHK(hipSetDevice(0));
     selected = true;
+    // set-up of the static scratch's address for this device, outside any later stream capture;
+    // a failure here is reported by the entry point that needs it (which retries), not by init
+    void *p;
+    if (scratch_resolve(&p)) g_err[0] = 0;
   }
   return 0;
 }
