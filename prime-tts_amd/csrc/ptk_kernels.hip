@@ -609,8 +609,11 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
     run(std::integral_constant<int, 0>{});
   }
 
-  // epilogue: the S partial sums of a block are added in wave order through LDS, then bias, the
-  // epilogue chain and one store per output
+  // Epilogue: the S partial sums of a block are added in wave order through LDS, then bias, the
+  // epilogue chain and one store per output.  Lane (l32, half) of a wave holds, for column block
+  // nb, the 16 values v of column q0 + 32*nb + l32 at rows 8*(v >> 2) + 4*half + (v & 3) of the
+  // 32-row block.  Wave ks of a column group finishes v in [v0, v0 + 16/S): groups g of four
+  // consecutive rows, v = v0 + 4*g + j (v0 is a multiple of 4).
   const long long qend = d.q0 + d.nq;
   const int M = d.M, C4 = d.C4, ys = d.ys, ypad = d.ypad, nepi = d.nepi;
   const long long Lout = d.Lout, ldy = d.ldy;
@@ -618,6 +621,127 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   float *y2b = d.y2 != nullptr ? d.y2 + (long long) b * d.bsy : nullptr;
   const float a2 = d.a2;
   const bool phase_rows = C4 != M;   // convT: row m is phase m / C4 of channel m % C4
+  // the tensor-add operand of the chain (the residual), if any
+  int addt = -1;
+  for (int e = 0; e < nepi; e++)
+    if (addt < 0 && d.epi[e].op == PTK_EPI_ADDT) addt = e;
+  const long long ldt = addt >= 0 ? d.epi[addt].ldt : 0;
+  const int nv = 16 / S, v0 = ks * nv, ngrp = nv / 4, wg0 = cg * S;
+
+  // Each wave writes its partial sums over its own staging area, which only it reads, so no wave
+  // waits for the others before writing (a separate region when NB column blocks do not fit).
+  constexpr bool OWN_RED = 16 * NB * 64 <= 8 * XWMAX;
+  auto red_of = [&](int wave) {
+    return OWN_RED ? smem + wave * 8 * XWMAX : smem + wave * NB * 16 * 64;
+  };
+  if constexpr (!OWN_RED) __syncthreads();
+  {
+    float *red = red_of(w);
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) red[(nb * 16 + v) * 64 + lane] = acc[nb][v];
+  }
+  auto reduce_wait = [&]() {
+    if (S > 1) {
+      __syncthreads();
+    } else {   // S = 1: a wave reads back only what it wrote
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  };
+
+  // Fast path: a full 32-row block whose rows are consecutive output channels (conv, or a convT
+  // block inside one phase, C4 a multiple of 32).  Every lane-dependent part of an output index
+  // (its column, whether that column exists) is computed once; row offsets are wave-uniform.
+  // The residual operands are all loaded before the reduction barrier, so their latency overlaps
+  // it (the compiler may not move a load past a store that could alias it; only the lane that
+  // writes an element reads its operand, so this is correct when the output overwrites it).
+  const bool fast = (!phase_rows || C4 % 32 == 0) && mb * 32 + 32 <= M && ldy < (1LL << 25) &&
+                    ldt < (1LL << 25);
+  if (fast) {
+    const int r_tile = phase_rows ? (mb * 32) / C4 : 0;
+    const long long row0 = (long long) mb * 32 - (long long) r_tile * C4;   // first channel
+    float *yk = yb + row0 * ldy;
+    float *y2k = y2b != nullptr ? y2b + row0 * ldy : nullptr;
+    const float *tk = addt >= 0 ? d.epi[addt].t + (long long) b * d.epi[addt].bst + row0 * ldt : nullptr;
+    const int ldy32 = (int) ldy, ldt32 = (int) ldt;
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+      const long long q = q0 + 32 * nb + l32;
+      const long long col = q * ys + r_tile - ypad;
+      const bool ok = q < qend && col >= 0 && col < Lout;
+      const int cl = ok ? (int) col : 0;
+      const int oy = 4 * half * ldy32 + cl, ot = 4 * half * ldt32 + cl;
+      float rv[4][4];
+      if (addt >= 0) {
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+          if (g < ngrp) {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+              rv[g][j] = ok ? tk[ot + (8 * ((v0 >> 2) + g) + j) * ldt32] : 0.0f;
+          }
+      }
+      if (nb == 0) reduce_wait();
+      float val[4][4];
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+        if (g < ngrp) {
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const int v = v0 + 4 * g + j;
+            float sum = red_of(wg0)[(nb * 16 + v) * 64 + lane];
+#pragma unroll
+            for (int i = 1; i < 4; i++)
+              if (i < S) sum += red_of(wg0 + i)[(nb * 16 + v) * 64 + lane];
+            val[g][j] = sum + bsh[8 * (v >> 2) + 4 * half + j];
+          }
+        }
+      for (int e = 0; e < nepi; e++) {
+        const int op = d.epi[e].op;
+        const float a = d.epi[e].a;
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+          if (g < ngrp) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              float x = val[g][j];
+              switch (op) {
+                case PTK_EPI_LEAKY: x = x >= 0.0f ? x : a * x; break;
+                case PTK_EPI_RELU: x = x > 0.0f ? x : 0.0f; break;
+                case PTK_EPI_MULS: x = x * a; break;
+                case PTK_EPI_ADDS: x = x + a; break;
+                case PTK_EPI_ADDT: x = e == addt ? x + rv[g][j]
+                                                 : x + d.epi[e].t[(long long) b * d.epi[e].bst +
+                                                                  (row0 + 8 * ((v0 >> 2) + g) + 4 * half + j) * d.epi[e].ldt + cl];
+                  break;
+                case PTK_EPI_DIVS: x = x / a; break;
+                default: break;
+              }
+              val[g][j] = x;
+            }
+          }
+      }
+      if (ok) {
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+          if (g < ngrp) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              const int o = oy + (8 * ((v0 >> 2) + g) + j) * ldy32;
+              yk[o] = val[g][j];
+              if (y2k != nullptr) y2k[o] = val[g][j] >= 0.0f ? val[g][j] : a2 * val[g][j];
+            }
+          }
+      }
+    }
+    return;
+  }
+
+  // General path (partial row blocks, convT phases that straddle a block): per element
+  reduce_wait();
   auto emit = [&](int nb, int v, float sum) {
     const int m = mb * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
     const long long q = q0 + 32 * nb + l32;
@@ -635,22 +759,12 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
     yb[yi] = val;
     if (y2b != nullptr) y2b[yi] = val >= 0.0f ? val : a2 * val;
   };
-  // S = 1 takes the same path (each wave reads its own block back): one rolled store loop keeps
-  // the kernel's code small
-  __syncthreads();
-  float *red = smem;
-#pragma unroll
-  for (int nb = 0; nb < NB; nb++)
-#pragma unroll
-    for (int v = 0; v < 16; v++) red[((w * NB + nb) * 16 + v) * 64 + lane] = acc[nb][v];
-  __syncthreads();
-  const int nv = 16 / S, v0 = ks * nv, wg0 = cg * S;
 #pragma unroll
   for (int nb = 0; nb < NB; nb++)
     for (int vv = 0; vv < nv; vv++) {
       const int v = v0 + vv;
-      float sum = red[((wg0 * NB + nb) * 16 + v) * 64 + lane];
-      for (int i = 1; i < S; i++) sum += red[(((wg0 + i) * NB + nb) * 16 + v) * 64 + lane];
+      float sum = red_of(wg0)[(nb * 16 + v) * 64 + lane];
+      for (int i = 1; i < S; i++) sum += red_of(wg0 + i)[(nb * 16 + v) * 64 + lane];
       emit(nb, v, sum);
     }
 }
