@@ -323,6 +323,65 @@ def _cpu_model():
     return "unknown"
 
 
+def queue_leg(pkg, lib, model, zs, wv, Ts, T_long, arena, args):
+    """Config 5's requests through ptd_queue (all submitted at the start of a step, long-form
+    last, deadline = submission time): step wall time, the long-form job's time to first audio
+    (its 48-frame first window complete) and every request's latency, medians over the steps."""
+    WF, WIN, CTX = 48, 96, 16
+    arena = max(arena, int(lib.ptd_windows2_arena_bytes(T_long, WF, WIN, CTX)))
+    q = lib.ptd_queue_create(model.ptr, len(Ts) + 1, arena, 64)
+    if not q:
+        raise RuntimeError("ptd_queue_create failed")
+    jobs = [pkg.Job(zs[i].ptr, wv[i].ptr, T, 0, 0, 0, 0.0) for i, T in enumerate(Ts)]
+    jobs.append(pkg.Job(zs[-1].ptr, wv[-1].ptr, T_long, WF, WIN, CTX, 0.0))
+    walls, ttfa, lat = [], [], []
+
+    def step():
+        ids = []
+        for j in jobs:
+            j.deadline_ms = lib.ptd_now_ms()
+            ids.append(lib.ptd_queue_submit(q, C.byref(j)))
+            if ids[-1] < 0:
+                raise RuntimeError("ptd_queue_submit refused a job")
+        sts = []
+        for i in ids:
+            st = pkg.JobStatus()
+            if lib.ptd_queue_wait(q, i, C.byref(st)) != 0 or st.rc != 0:
+                raise RuntimeError("queue job failed")
+            sts.append(st)
+        t0 = min(st.t_submit for st in sts)
+        return (max(st.t_end for st in sts) - t0, sts[-1].t_first - sts[-1].t_submit,
+                [st.t_end - st.t_submit for st in sts[:-1]])
+
+    try:
+        for _ in range(args.warmup):
+            step()
+        for _ in range(args.steps):
+            w, f, l8 = step()
+            walls.append(w)
+            ttfa.append(f)
+            lat.extend(l8)
+        # the long-form job alone on an idle queue: its first window without the load
+        alone = []
+        for _ in range(5):
+            jl = jobs[-1]
+            jl.deadline_ms = lib.ptd_now_ms()
+            i = lib.ptd_queue_submit(q, C.byref(jl))
+            st = pkg.JobStatus()
+            if i < 0 or lib.ptd_queue_wait(q, i, C.byref(st)) != 0 or st.rc != 0:
+                raise RuntimeError("queue job failed")
+            alone.append(st.t_first - st.t_submit)
+    finally:
+        lib.ptd_queue_destroy(q)
+    audio = (sum(Ts) + T_long) * HOP / SR
+    med = lambda xs: float(np.median(xs))
+    return {"workers": len(Ts) + 1, "longform_windows": f"{WF} then {WIN}, ctx {CTX}",
+            "ms_per_step": round(med(walls), 4), "audio_s_per_s": round(audio / (med(walls) / 1e3), 2),
+            "longform_first_audio_ms": round(med(ttfa), 4), "longform_first_audio_max_ms": round(max(ttfa), 4),
+            "longform_first_audio_idle_ms": round(med(alone), 4),
+            "request_latency_ms": {"median": round(med(lat), 4), "max": round(max(lat), 4)}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -590,6 +649,15 @@ def main():
               "config5_longform_windows_vs_full_decode_sndr_db": round(sndr_db(c5_wavs[-1], dfull.download(ctx)), 2)}
     dfull.free()
     lib.ptd_server_destroy(srv)
+
+    # ---------------------------------------------------------------- config 5 through the queue
+    # The same nine requests submitted to the queue-fed server (ptd_queue: 9 persistent workers,
+    # earliest-deadline-first, deadline = arrival time), the long-form request as a streaming job
+    # with the reference's short first window (48 frames, then 96-frame windows, 16 of context).
+    # Reported beside the value, not in it: time to first audio under this load, per-request
+    # latency, and the throughput of the queue path.
+    queue = queue_leg(pkg, lib, model, zs, wv, Ts, T_long, arena, args)
+    log(f"queue: {queue}")
     for b in zs + wv:
         b.free()
 
@@ -629,6 +697,7 @@ def main():
             "alg_bytes_per_request": tail_bytes(TAIL_L, 1), **tail,
         },
         "streaming": stream,
+        "serving_queue": queue,
         "container_load": container,
         "matmul_us_per_call": mm,
         **cfg,

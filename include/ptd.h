@@ -133,6 +133,15 @@ int ptd_mrf_depth(pt_ctx *c, const ptd_model *m, int stage, int depth, const flo
 int ptd_decode_windows(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int win, int ctx,
                        float *wav);
 size_t ptd_windows_arena_bytes(int64_t T, int win, int ctx);
+/* The same with the reference's streaming schedule (main_v21_serve.c:219-257): the first window
+ * win_first frames wide (fast first audio; the reference's default 48), the later ones win (its
+ * default 256), both >= 2*ctx + 1.  The first window runs as its own decode when its width
+ * differs, the evenly spaced full windows as one batched decode, a clipped last window alone.
+ * Output identical to decoding the windows one at a time (ptd_decode_chunk) and keeping what the
+ * reference's loop keeps.  Asynchronous.  0 / -1. */
+int ptd_decode_windows2(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int win_first,
+                        int win, int ctx, float *wav);
+size_t ptd_windows2_arena_bytes(int64_t T, int win_first, int win, int ctx);
 
 /* A decode of fixed shape and buffers captured once as a HIP graph and replayed (no counterpart in
  * the reference, whose graph interpreter issues every node from the host): for a serving loop that
@@ -173,6 +182,45 @@ typedef struct {
 } ptd_request;
 int ptd_serve_run(ptd_server *s, const ptd_model *m, const ptd_request *req, int nreq,
                   double *wall_ms);
+
+/* ---- queue-fed serving (the reference's server loop, main_v21_serve.c:129-160, :281-335) --- *
+ * nworkers persistent workers, each with its own context (stream + arena) sharing the model,
+ * created once with the queue.  Jobs are submitted with a deadline and popped earliest-deadline-
+ * first (stable: equal deadlines keep submission order), as the reference's EDF queue does; the
+ * queue holds at most `capacity` unfinished jobs (queued or running; the reference's MAX_QUEUE is
+ * 64) and refuses more.  A job either decodes in one piece or streams: win > 0 runs the
+ * overlap-save schedule of ptd_decode_windows2 with its first window decoded, and waited for, on
+ * its own, so its audio (the first win_first - ctx frames) is complete at t_first, and the rest
+ * batched.  All times are ptd_now_ms() values. */
+typedef struct ptd_queue ptd_queue;
+typedef struct {
+  const float *z;        /* device [192][T], read in place; valid until the job is done */
+  float *wav;            /* device [256*T] */
+  int64_t T;
+  int win_first, win, ctx;   /* win > 0: streaming windows; win == 0: one decode */
+  double deadline_ms;    /* EDF key: smaller runs first */
+} ptd_job;
+typedef struct {
+  int rc;                /* the job's result: 0 / -1 */
+  int worker;            /* which worker ran it */
+  int64_t order;         /* 0, 1, 2, ...: the order in which workers took jobs from the queue */
+  double t_submit, t_start, t_first, t_end;   /* t_first: first audio complete (= t_end unless
+                                                streaming) */
+} ptd_job_status;
+/* NULL on failure (every context released) */
+ptd_queue *ptd_queue_create(const ptd_model *m, int nworkers, size_t arena_bytes, int capacity);
+/* job id (>= 0), or -1 when the queue is full, closed or the job is malformed */
+int64_t ptd_queue_submit(ptd_queue *q, const ptd_job *job);
+/* 1 done (status filled, the job's slot released), 0 still queued or running, -1 unknown id */
+int ptd_queue_poll(ptd_queue *q, int64_t id, ptd_job_status *st);
+/* blocks until the job is done; 0 (status filled, slot released) or -1 unknown id */
+int ptd_queue_wait(ptd_queue *q, int64_t id, ptd_job_status *st);
+/* hold = 1: workers take no new job (running ones finish); 0: resume.  For a caller that submits
+ * a batch of jobs and wants them ordered among themselves by deadline. */
+void ptd_queue_hold(ptd_queue *q, int hold);
+/* runs every queued job, joins the workers, releases the contexts */
+void ptd_queue_destroy(ptd_queue *q);
+double ptd_now_ms(void);   /* host clock of the job times */
 
 /* ---- plumbing for callers without a HIP runtime of their own (tests, bench.py) ------------ */
 void *ptd_malloc(size_t bytes);                 /* device memory, NULL on failure */

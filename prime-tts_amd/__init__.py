@@ -74,6 +74,15 @@ _SIGS = {
     "ptd_device_sync": (C.c_int, []),
     "ptd_decode_windows": (C.c_int, [VP, VP, VP, I64, C.c_int, C.c_int, VP]),
     "ptd_windows_arena_bytes": (C.c_size_t, [I64, C.c_int, C.c_int]),
+    "ptd_decode_windows2": (C.c_int, [VP, VP, VP, I64, C.c_int, C.c_int, C.c_int, VP]),
+    "ptd_windows2_arena_bytes": (C.c_size_t, [I64, C.c_int, C.c_int, C.c_int]),
+    "ptd_queue_create": (VP, [VP, C.c_int, C.c_size_t, C.c_int]),
+    "ptd_queue_destroy": (None, [VP]),
+    "ptd_queue_hold": (None, [VP, C.c_int]),
+    "ptd_queue_submit": (I64, [VP, VP]),
+    "ptd_queue_poll": (C.c_int, [VP, I64, VP]),
+    "ptd_queue_wait": (C.c_int, [VP, I64, VP]),
+    "ptd_now_ms": (C.c_double, []),
     "ptd_decode_chunk": (C.c_int, [VP, VP, VP, I64, I64, I64, VP, C.POINTER(I64)]),
     "ptd_decode_graph": (VP, [VP, VP, VP, I64, C.c_int, VP]),
     "ptd_graph_launch": (C.c_int, [VP, VP]),
@@ -107,6 +116,18 @@ TAIL_NCONST = 16 + 144 + 144   # closed-form part of the tail table (Hann, irfft
 
 class Request(C.Structure):
     _fields_ = [("z", VP), ("wav", VP), ("T", I64), ("win", C.c_int), ("ctx", C.c_int)]
+
+
+class Job(C.Structure):
+    """ptd_job: one decode request for ptd_queue_submit (win > 0: streaming windows)."""
+    _fields_ = [("z", VP), ("wav", VP), ("T", I64), ("win_first", C.c_int), ("win", C.c_int),
+                ("ctx", C.c_int), ("deadline_ms", C.c_double)]
+
+
+class JobStatus(C.Structure):
+    """ptd_job_status: result and host times (ptd_now_ms) of a finished queue job."""
+    _fields_ = [("rc", C.c_int), ("worker", C.c_int), ("order", I64), ("t_submit", C.c_double),
+                ("t_start", C.c_double), ("t_first", C.c_double), ("t_end", C.c_double)]
 
 
 _lib = None

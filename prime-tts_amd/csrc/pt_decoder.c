@@ -468,19 +468,21 @@ int ptd_mrf(pt_ctx *c, const ptd_model *m, int stage, const float *x, int64_t T,
 }
 
 /* ------------------------------------------------------------------ overlap-save windows
- * The reference's window schedule (main_v21_serve.c:229-257): window at frame a covers
- * [a, a + min(win, T - a)); it emits [max(a + lo, emitted), min(a + hi, T)) with lo = ctx except
+ * The reference's window schedule (main_v21_serve.c:219-257): the first window is win_first
+ * frames wide (fast first audio), later ones win; window at frame a covers
+ * [a, a + min(width, T - a)); it emits [max(a + lo, emitted), min(a + hi, T)) with lo = ctx except
  * for the first window, hi = width - ctx except for the last; the next window starts at
- * emitted - ctx.  Windows of equal width run as one batched decode. */
+ * emitted - ctx.  Windows of equal width after the first are evenly spaced (hop = win - 2*ctx)
+ * and run as one batched decode. */
 typedef struct {
   int64_t a, w, e0, e1;
 } win_t;
 
-static int win_schedule(int64_t T, int win, int ctx, win_t *out, int cap) {
+static int win_schedule(int64_t T, int win_first, int win, int ctx, win_t *out, int cap) {
   int n = 0;
   int64_t a = 0, emitted = 0;
   while (emitted < T && n < cap) {
-    int64_t w = win;
+    int64_t w = a == 0 ? win_first : win;
     if (a + w > T) w = T - a;
     const int last = a + w >= T;
     const int64_t lo = a == 0 ? 0 : ctx, hi = last ? w : w - ctx;
@@ -502,60 +504,127 @@ static int win_schedule(int64_t T, int win, int ctx, win_t *out, int cap) {
 
 #define MAX_WIN 4096
 
-/* The windows of one sequence: the full-width ones start at a = i*hop (hop = win - 2*ctx) and run
- * as one batched decode that reads z in place (batch stride hop) and writes each window's kept
- * frames straight to their place in wav (item stride hop*256); a shorter last window runs as a
- * second decode.  No copies. */
-size_t ptd_windows_arena_bytes(int64_t T, int win, int ctx) {
-  win_t *w = malloc(sizeof(win_t) * MAX_WIN);
-  if (!w) return 0;
-  const int n = win_schedule(T, win, ctx, w, MAX_WIN);
-  int nfull = 0;
-  size_t tail = 0;
-  for (int i = 0; i < n; i++) {
-    if (w[i].w == win) nfull++;
-    else tail = ptd_decode_arena_bytes(w[i].w, 1);
+/* A schedule split into the launches that run it: the first window (alone when its width differs
+ * from the others, or when asked to), then a run of full-width windows at a constant hop (one
+ * batched decode reading z in place with batch stride hop and writing each window's kept frames
+ * to their place in wav), then at most one shorter last window. */
+typedef struct {
+  int n;             /* windows */
+  int first_alone;   /* window 0 decoded on its own */
+  int b0, nfull;     /* the batched run: windows [b0, b0 + nfull) */
+  int has_last;      /* window n - 1 clipped, decoded on its own */
+  int64_t hop;
+  win_t w0, wl, wb0;
+} win_plan;
+
+static int win_plan_make(int64_t T, int win_first, int win, int ctx, int split_first,
+                         win_plan *pl) {
+  memset(pl, 0, sizeof *pl);
+  if (T < 1 || ctx < 0 || win < 2 * ctx + 1 || win_first < 2 * ctx + 1) return -1;
+  win_t *ws = malloc(sizeof(win_t) * MAX_WIN);
+  if (!ws) return -1;
+  const int n = win_schedule(T, win_first, win, ctx, ws, MAX_WIN);
+  pl->n = n;
+  pl->hop = win - 2 * ctx;
+  pl->w0 = ws[0];
+  pl->first_alone = split_first || win_first != win || ws[0].w != win;
+  int i = pl->first_alone ? 1 : 0;
+  pl->b0 = i;
+  while (i < n && ws[i].w == win) i++;
+  pl->nfull = i - pl->b0;
+  pl->has_last = i < n;
+  if (pl->nfull) pl->wb0 = ws[pl->b0];
+  if (pl->has_last) pl->wl = ws[n - 1];
+  int rc = (n < MAX_WIN && i + (pl->has_last ? 1 : 0) == n) ? 0 : -1;
+  /* the invariants the batched run relies on: constant hop, kept frames [a + lo, a + win - ctx)
+   * (lo = 0 only for window 0), a full last window keeps up to a + win */
+  for (int k = pl->b0; rc == 0 && k < pl->b0 + pl->nfull; k++) {
+    const int64_t lo = k ? ctx : 0, hi = (k + 1 == n) ? win : win - ctx;
+    if (ws[k].a != pl->wb0.a + (k - pl->b0) * pl->hop || ws[k].e0 != ws[k].a + lo ||
+        ws[k].e1 != ws[k].a + hi)
+      rc = -1;
   }
-  free(w);
-  const size_t full = nfull ? ptd_decode_arena_bytes(win, nfull) : 0;
-  return (full > tail ? full : tail) + 4096;
+  free(ws);
+  if (rc) PT_LOG("windowed decode: unexpected window schedule (T %lld win %d/%d ctx %d)",
+                 (long long) T, win_first, win, ctx);
+  return rc;
+}
+
+static size_t win_plan_arena(const win_plan *pl, int win) {
+  size_t b = 0, x;
+  if (pl->first_alone && (x = ptd_decode_arena_bytes(pl->w0.w, 1)) > b) b = x;
+  if (pl->nfull && (x = ptd_decode_arena_bytes(win, pl->nfull)) > b) b = x;
+  if (pl->has_last && (x = ptd_decode_arena_bytes(pl->wl.w, 1)) > b) b = x;
+  return b + 4096;
+}
+
+/* one window decoded on its own, writing its kept frames to their place in wav */
+static int win_one(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, const win_t *l,
+                   float *wav) {
+  const ptk_emit em = {(l->e0 - l->a) * 256, 0, (l->e1 - l->a) * 256, (l->e1 - l->a) * 256};
+  return decode_impl(c, m, z + l->a, T, 0, l->w, 1, wav + l->a * 256, 0, &em, NULL);
+}
+
+/* the batched run of full-width windows */
+static int win_batch(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, const win_plan *pl,
+                     int win, int ctx, float *wav) {
+  const int last_full = pl->b0 + pl->nfull == pl->n;
+  const ptk_emit em = {pl->b0 == 0 ? 0 : (int64_t) ctx * 256, (int64_t) ctx * 256,
+                       (int64_t) (win - ctx) * 256,
+                       (int64_t) (last_full ? win : win - ctx) * 256};
+  return decode_impl(c, m, z + pl->wb0.a, T, pl->hop, win, pl->nfull, wav + pl->wb0.a * 256,
+                     pl->hop * 256, &em, NULL);
+}
+
+size_t ptd_windows2_arena_bytes(int64_t T, int win_first, int win, int ctx) {
+  win_plan pl;
+  /* the plan with the first window split off needs at least what the merged one needs */
+  if (win_plan_make(T, win_first, win, ctx, 1, &pl)) return 0;
+  size_t b = win_plan_arena(&pl, win);
+  if (win_first == win && win_plan_make(T, win_first, win, ctx, 0, &pl) == 0) {
+    const size_t b2 = win_plan_arena(&pl, win);
+    if (b2 > b) b = b2;
+  }
+  return b;
+}
+
+size_t ptd_windows_arena_bytes(int64_t T, int win, int ctx) {
+  return ptd_windows2_arena_bytes(T, win, win, ctx);
+}
+
+/* The windows of one sequence, in as few launches as the schedule allows.  t_first (optional):
+ * window 0 is decoded alone and waited for, and the host time its audio was complete is stored
+ * (the reference's fast first audio, main_v21_serve.c:219-225); the rest follows batched. */
+int ptdi_decode_windows(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int win_first,
+                        int win, int ctx, float *wav, double *t_first) {
+  if (!c || !c->use_cuda || !m || !z || !wav) return -1;
+  win_plan pl;
+  if (win_plan_make(T, win_first, win, ctx, t_first != NULL, &pl)) return -1;
+  int rc = 0;
+  if (pl.first_alone) {
+    rc = win_one(c, m, z, T, &pl.w0, wav);
+    if (rc == 0 && t_first) {
+      rc = ptdi_wait(c);
+      *t_first = ptdi_now_ms();
+    }
+  }
+  /* the shorter last window before the batched run: a small decode that leaves most of the chip
+   * to other streams is better early than as the tail of the request (windows write disjoint
+   * samples) */
+  if (rc == 0 && pl.has_last) rc = win_one(c, m, z, T, &pl.wl, wav);
+  if (rc == 0 && pl.nfull) rc = win_batch(c, m, z, T, &pl, win, ctx, wav);
+  if (rc) PT_LOG("windowed decode failed: %s", ptk_last_error());
+  return rc;
 }
 
 int ptd_decode_windows(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int win, int ctx,
                        float *wav) {
-  if (!c || !c->use_cuda || !m || T < 1 || win < 2 * ctx + 1 || ctx < 0) return -1;
-  win_t *ws = malloc(sizeof(win_t) * MAX_WIN);
-  if (!ws) return -1;
-  const int n = win_schedule(T, win, ctx, ws, MAX_WIN);
-  const int64_t hop = win - 2 * ctx;
-  int rc = 0, nfull = 0;
-  while (nfull < n && ws[nfull].w == win) nfull++;
-  /* the schedule's invariants this relies on: full windows first, evenly spaced, kept frames
-   * [a + (i ? ctx : 0), a + win - ctx) except a full last window, which keeps up to a + win */
-  for (int i = 0; i < nfull; i++) {
-    const int64_t lo = i ? ctx : 0, hi = (i + 1 == n) ? win : win - ctx;
-    if (ws[i].a != i * hop || ws[i].e0 != ws[i].a + lo || ws[i].e1 != ws[i].a + hi) rc = -1;
-  }
-  if (rc || nfull + 1 < n) {
-    PT_LOG("windowed decode: unexpected window schedule (T %lld win %d ctx %d)", (long long) T, win, ctx);
-    free(ws);
-    return -1;
-  }
-  /* the shorter last window first: a small decode that leaves most of the chip to other streams
-   * is better early than as the tail of the request (the windows write disjoint samples) */
-  if (nfull < n) {
-    const win_t *l = &ws[n - 1];
-    const ptk_emit em = {(l->e0 - l->a) * 256, 0, (l->e1 - l->a) * 256, (l->e1 - l->a) * 256};
-    rc = decode_impl(c, m, z + l->a, T, 0, l->w, 1, wav + l->a * 256, 0, &em, NULL);
-  }
-  if (rc == 0 && nfull) {
-    const ptk_emit em = {0, (int64_t) ctx * 256, (int64_t) (win - ctx) * 256,
-                         (int64_t) (nfull == n ? win : win - ctx) * 256};
-    rc = decode_impl(c, m, z, T, hop, win, nfull, wav, hop * 256, &em, NULL);
-  }
-  if (rc) PT_LOG("windowed decode failed: %s", ptk_last_error());
-  free(ws);
-  return rc;
+  return ptdi_decode_windows(c, m, z, T, win, win, ctx, wav, NULL);
+}
+
+int ptd_decode_windows2(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int win_first,
+                        int win, int ctx, float *wav) {
+  return ptdi_decode_windows(c, m, z, T, win_first, win, ctx, wav, NULL);
 }
 
 /* ------------------------------------------------------------------ captured decodes

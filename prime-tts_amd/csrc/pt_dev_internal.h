@@ -62,4 +62,9 @@ int ptdi_ctx_init(pt_ctx *c, size_t arena_bytes, int verbose);
 /* elapsed wall-clock ms since an arbitrary origin */
 double ptdi_now_ms(void);
 
+/* windowed decode with the reference's first / later widths; t_first != NULL: window 0 is
+ * decoded alone, waited for, and its completion time stored there */
+int ptdi_decode_windows(pt_ctx *c, const struct ptd_model *m, const float *z, int64_t T,
+                        int win_first, int win, int ctx, float *wav, double *t_first);
+
 #endif
