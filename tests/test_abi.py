@@ -80,3 +80,23 @@ def test_host_only_calls_fail_loudly_without_device():
                          1, pkg.fptr(w), pkg.fptr(None), 1, -1, -1, 0, 0, 0.0, 0.0)
     assert rc == -1
     assert np.all(y == 0)
+
+
+def test_pads_in_kernel_follows_the_op_switch():
+    """PT_V21_GPU without "conv" routes convs to the host's CPU path, which reads padded rows, so the
+    library tells the host to pad (pt_v21_conv_pads_in_kernel = 0); by default it pads in-kernel.
+    No device call: run in child processes with the environment set."""
+    import subprocess
+    import sys
+    code = ("import ctypes, sys; lib = ctypes.CDLL(sys.argv[1]); "
+            "print(lib.pt_v21_conv_pads_in_kernel(None))")
+    lib = str(ROOT / "prime-tts_amd" / "libptconv_hip.so")
+    out = {}
+    for v in (None, "conv,convT,matmul", "convT", "matmul", ""):
+        env = {k: x for k, x in __import__("os").environ.items() if k != "PT_V21_GPU"}
+        if v is not None:
+            env["PT_V21_GPU"] = v
+        r = subprocess.run([sys.executable, "-c", code, lib], env=env, capture_output=True,
+                           text=True, timeout=60)
+        out[v] = int(r.stdout.strip())
+    assert out == {None: 1, "conv,convT,matmul": 1, "convT": 1, "matmul": 0, "": 1}

@@ -85,6 +85,34 @@ def test_reference_driver_through_the_library(model, tmp_path, mode):
     assert "pt_v21 hip: context ready" in r.stderr
 
 
+# PT_V21_GPU, the reference's per-op bisection switch (pt_v21_cuda.cu:70-76; substring test, so
+# "conv" keeps conv and drops convT): the ops it leaves out run on the host's CPU path
+ROUTES = {"matmul_only": ("matmul", {"conv", "convT"}), "conv_only": ("conv", {"convT"})}
+
+
+@pytest.mark.parametrize("route", list(ROUTES))
+def test_reference_driver_per_op_routing(model, tmp_path, route):
+    """With convs routed to the CPU path the library answers pt_v21_conv_pads_in_kernel = 0, so the
+    host pads rows and chains nothing, and the host's CPU conv gets the rows it expects; the
+    waveform still passes the driver's gate.  The routed ops take host-CPU time (the device path
+    needs a few ms for the whole graph), which shows they really ran there."""
+    d, case, cpu_wav = model
+    value, on_cpu = ROUTES[route]
+    say(f"reference driver with PT_V21_GPU={value}")
+    r = _run([DEV_BIN, "--container", d / "model.ptk", "--case", case, "--out", tmp_path / "w.npy"],
+             600, {"PT_V21_GPU": value})
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    a, b = np.load(tmp_path / "w.npy").ravel(), np.load(cpu_wav).ravel()
+    assert a.shape == b.shape and np_ref.sndr(a, b) >= 60.0
+    m = re.search(r"conv=(\d+) convT=(\d+) matmul=(\d+)\s+conv ([0-9.]+) ms\s+convT ([0-9.]+) ms", r.stdout)
+    assert m, r.stdout[-2000:]
+    assert tuple(int(v) for v in m.groups()[:3]) == (124, 5, 50)
+    conv_ms, convT_ms = float(m.group(4)), float(m.group(5))
+    say(f"conv {conv_ms} ms, convT {convT_ms} ms")
+    assert (conv_ms > 100.0) == ("conv" in on_cpu)
+    assert (convT_ms > 20.0) == ("convT" in on_cpu)
+
+
 def test_reference_driver_gpu_split(model, tmp_path):
     """PT_V21_CUDAPROF=1, the reference's phase profiler: the linked driver prints its own
     "gpu split" line from the context fields this library fills (alloc / copy / kernel+sync /
