@@ -497,19 +497,23 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
 
   // Staging is split so that all global loads of a chunk are in flight together: the load phase
   // only issues loads, the store phase (one chunk later) transforms and writes LDS.
+  // Rows past cin exist only when cin is not a multiple of 32 (cinp > cin); MASK (compile time)
+  // selects the chunk code that handles them, so the common case carries no per-row tests.
   float pf[CONV_CK][NJ];
-  auto load_chunk = [&](int c0) {
+  auto load_chunk = [&](int c0, auto mask) {
+    constexpr bool MASK = decltype(mask)::value;
 #pragma unroll
     for (int r = 0; r < CONV_CK; r++) {
-      const unsigned rowo = c0 + r < cin ? (unsigned) (c0 + r) * ldx4 : 0u;
+      const unsigned rowo = (!MASK || c0 + r < cin) ? (unsigned) (c0 + r) * ldx4 : 0u;
 #pragma unroll
       for (int jj = 0; jj < NJ; jj++) {
         pf[r][jj] = buf_load(rx, voff[jj], rowo);
       }
     }
   };
-  auto store_chunk = [&](int c0) {
-    const int nlive = cin - c0;   // rows of this chunk that hold channels (8 unless cin % 8 != 0)
+  auto store_chunk = [&](int c0, auto mask) {
+    constexpr bool MASK = decltype(mask)::value;
+    const int nlive = cin - c0;   // rows of this chunk that hold channels
 #pragma unroll
     for (int jj = 0; jj < NJ; jj++) {
       float v[CONV_CK];
@@ -517,9 +521,11 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
       for (int r = 0; r < CONV_CK; r++) {
         v[r] = in_xform<IN>(pf[r][jj], in_a);
       }
-      if (nlive < CONV_CK) {
+      if constexpr (MASK) {
+        if (nlive < CONV_CK) {
 #pragma unroll
-        for (int r = 0; r < CONV_CK; r++) v[r] = r < nlive ? v[r] : 0.0f;
+          for (int r = 0; r < CONV_CK; r++) v[r] = r < nlive ? v[r] : 0.0f;
+        }
       }
       xs[lane + 64 * jj] = make_float4(v[0], v[2], v[4], v[6]);
       xs[XWMAX + lane + 64 * jj] = make_float4(v[1], v[3], v[5], v[7]);
@@ -561,19 +567,19 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   // chunk's window loads, then per tap four MFMAs on acur[k] followed by the load of that tap's
   // operands for the next chunk into the same registers (prefetch distance about one chunk).  The
   // last chunk is peeled so it issues no loads.
-  auto run = [&](auto kc) {
+  auto run = [&](auto kc, auto mask) {
     constexpr int KC = decltype(kc)::value;
     constexpr int KA = KC > 0 ? KC : 1;
     float4 acur[KA];
     auto chunk = [&](int j, auto with_loads) {
       constexpr bool LD = decltype(with_loads)::value;
       __builtin_amdgcn_wave_barrier();
-      store_chunk((chunk0 + j) * CONV_CK);
+      store_chunk((chunk0 + j) * CONV_CK, mask);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       if constexpr (LD) {
-        load_chunk((chunk0 + j + 1) * CONV_CK);
+        load_chunk((chunk0 + j + 1) * CONV_CK, mask);
         PTK_PIN_VMEM();
       }
       if constexpr (KC > 0) {
@@ -592,7 +598,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
     };
     // window loads first, then the A operands: the same order as inside a chunk, so the wait
     // before the first window store is the same count on entry as on every later trip
-    load_chunk(chunk0 * CONV_CK);
+    load_chunk(chunk0 * CONV_CK, mask);
     if constexpr (KC > 0) {
 #pragma unroll
       for (int k = 0; k < KC; k++) acur[k] = wa(k, 0);
@@ -600,13 +606,19 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
     for (int j = 0; j + 1 < nch; j++) chunk(j, std::true_type{});
     chunk(nch - 1, std::false_type{});
   };
-  if constexpr (KT > 0) {
-    if (K == KT) run(std::integral_constant<int, KT>{});
-    else if (KT > 7 && K == 7) run(std::integral_constant<int, 7>{});
-    else if (KT > 3 && K == 3) run(std::integral_constant<int, 3>{});
-    else run(std::integral_constant<int, 0>{});
+  if (cin == d.cinp) {
+    constexpr std::false_type nomask{};
+    if constexpr (KT > 0) {
+      if (K == KT) run(std::integral_constant<int, KT>{}, nomask);
+      else if (KT > 7 && K == 7) run(std::integral_constant<int, 7>{}, nomask);
+      else if (KT > 3 && K == 3) run(std::integral_constant<int, 3>{}, nomask);
+      else run(std::integral_constant<int, 0>{}, nomask);
+    } else {
+      run(std::integral_constant<int, 0>{}, nomask);
+    }
   } else {
-    run(std::integral_constant<int, 0>{});
+    // channel padding in the last chunks: any K through the generic body
+    run(std::integral_constant<int, 0>{}, std::true_type{});
   }
 
   // Epilogue: the S partial sums of a block are added in wave order through LDS, then bias, the
