@@ -499,23 +499,27 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   // only issues loads, the store phase (one chunk later) transforms and writes LDS.
   // Rows past cin exist only when cin is not a multiple of 32 (cinp > cin); MASK (compile time)
   // selects the chunk code that handles them, so the common case carries no per-row tests.
+  // NJU (compile time) of the NJ slices are staged: windows up to 64 columns (every decoder conv
+  // but K = 11 at dilation 5) need one, which halves the window loads and LDS stores.
   float pf[CONV_CK][NJ];
-  auto load_chunk = [&](int c0, auto mask) {
+  auto load_chunk = [&](int c0, auto mask, auto nju) {
     constexpr bool MASK = decltype(mask)::value;
+    constexpr int NJU = decltype(nju)::value;
 #pragma unroll
     for (int r = 0; r < CONV_CK; r++) {
       const unsigned rowo = (!MASK || c0 + r < cin) ? (unsigned) (c0 + r) * ldx4 : 0u;
 #pragma unroll
-      for (int jj = 0; jj < NJ; jj++) {
+      for (int jj = 0; jj < NJU; jj++) {
         pf[r][jj] = buf_load(rx, voff[jj], rowo);
       }
     }
   };
-  auto store_chunk = [&](int c0, auto mask) {
+  auto store_chunk = [&](int c0, auto mask, auto nju) {
     constexpr bool MASK = decltype(mask)::value;
+    constexpr int NJU = decltype(nju)::value;
     const int nlive = cin - c0;   // rows of this chunk that hold channels
 #pragma unroll
-    for (int jj = 0; jj < NJ; jj++) {
+    for (int jj = 0; jj < NJU; jj++) {
       float v[CONV_CK];
 #pragma unroll
       for (int r = 0; r < CONV_CK; r++) {
@@ -567,19 +571,19 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   // chunk's window loads, then per tap four MFMAs on acur[k] followed by the load of that tap's
   // operands for the next chunk into the same registers (prefetch distance about one chunk).  The
   // last chunk is peeled so it issues no loads.
-  auto run = [&](auto kc, auto mask) {
+  auto run = [&](auto kc, auto mask, auto nju) {
     constexpr int KC = decltype(kc)::value;
     constexpr int KA = KC > 0 ? KC : 1;
     float4 acur[KA];
     auto chunk = [&](int j, auto with_loads) {
       constexpr bool LD = decltype(with_loads)::value;
       __builtin_amdgcn_wave_barrier();
-      store_chunk((chunk0 + j) * CONV_CK, mask);
+      store_chunk((chunk0 + j) * CONV_CK, mask, nju);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       if constexpr (LD) {
-        load_chunk((chunk0 + j + 1) * CONV_CK, mask);
+        load_chunk((chunk0 + j + 1) * CONV_CK, mask, nju);
         PTK_PIN_VMEM();
       }
       if constexpr (KC > 0) {
@@ -598,7 +602,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
     };
     // window loads first, then the A operands: the same order as inside a chunk, so the wait
     // before the first window store is the same count on entry as on every later trip
-    load_chunk(chunk0 * CONV_CK, mask);
+    load_chunk(chunk0 * CONV_CK, mask, nju);
     if constexpr (KC > 0) {
 #pragma unroll
       for (int k = 0; k < KC; k++) acur[k] = wa(k, 0);
@@ -606,19 +610,23 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
     for (int j = 0; j + 1 < nch; j++) chunk(j, std::true_type{});
     chunk(nch - 1, std::false_type{});
   };
+  constexpr std::false_type nomask{};
+  constexpr std::integral_constant<int, 1> one{};
+  constexpr std::integral_constant<int, NJ> all{};
+  const bool narrow = XW <= 64;
   if (cin == d.cinp) {
-    constexpr std::false_type nomask{};
     if constexpr (KT > 0) {
-      if (K == KT) run(std::integral_constant<int, KT>{}, nomask);
-      else if (KT > 7 && K == 7) run(std::integral_constant<int, 7>{}, nomask);
-      else if (KT > 3 && K == 3) run(std::integral_constant<int, 3>{}, nomask);
-      else run(std::integral_constant<int, 0>{}, nomask);
+      if (K == KT && narrow) run(std::integral_constant<int, KT>{}, nomask, one);
+      else if (K == KT) run(std::integral_constant<int, KT>{}, nomask, all);
+      else if (KT > 7 && K == 7 && narrow) run(std::integral_constant<int, 7>{}, nomask, one);
+      else if (KT > 3 && K == 3 && narrow) run(std::integral_constant<int, 3>{}, nomask, one);
+      else run(std::integral_constant<int, 0>{}, nomask, all);
     } else {
-      run(std::integral_constant<int, 0>{}, nomask);
+      run(std::integral_constant<int, 0>{}, nomask, all);
     }
   } else {
     // channel padding in the last chunks: any K through the generic body
-    run(std::integral_constant<int, 0>{}, std::true_type{});
+    run(std::integral_constant<int, 0>{}, std::true_type{}, all);
   }
 
   // Epilogue: the S partial sums of a block are added in wave order through LDS, then bias, the
