@@ -82,10 +82,17 @@ void ptd_tail_constants(float *out) {
 
 /* the final conv's taps h[band*63 + m] = W[0][band][m] out of its packed weight [1][63][4][4]
  * (row 0 of the first row block), then its bias (0 without one) */
+/* The final PQMF conv's taps in polyphase order: entry ((band * 4 + r) * 16 + j) is tap
+ * m = 3 - r + 4j of that band (0 for m = 63), the taps output sample 4u + r of a block multiplies
+ * with y slots u + 1 + j; then the bias. */
 static void tail_fir(float *dst, const float *wp, const float *bias) {
   for (int band = 0; band < 4; band++)
-    for (int m = 0; m < 63; m++) dst[band * 63 + m] = wp[((size_t) m * 4 + band) * 4 + 0];
-  dst[252] = bias ? bias[0] : 0.0f;
+    for (int r = 0; r < 4; r++)
+      for (int j = 0; j < 16; j++) {
+        const int m = 3 - r + 4 * j;
+        dst[(band * 4 + r) * 16 + j] = m < 63 ? wp[((size_t) m * 4 + band) * 4 + 0] : 0.0f;
+      }
+  dst[256] = bias ? bias[0] : 0.0f;
 }
 
 static void layer_gemm(const layer_geo *g, int *M, int *K) {

@@ -160,9 +160,10 @@ typedef struct {
 /* batched: item b reads p + b*bsp and writes wav + b*bsw */
 int ptk_tail_batched(const float *p, int64_t ldp, int64_t bsp, int64_t L, float *wav, int64_t bsw,
                      int batch, const float *consts, const ptk_emit *emit, void *s);
-/* the tail's table (floats): hann[16], basis_c[9*16], basis_s[9*16], the final conv's taps
- * h[band*63 + m] (252) and its bias (1) */
-#define PTK_TAIL_NCONST (16 + 144 + 144 + 252 + 1)
+/* the tail's table (floats): hann[16], basis_c[9*16], basis_s[9*16], the final conv's taps in
+ * polyphase order hp[(band*4 + r)*16 + j] = tap 3 - r + 4j of the band (0 past tap 62; 256), and
+ * its bias (1) */
+#define PTK_TAIL_NCONST (16 + 144 + 144 + 256 + 1)
 
 /* lane-layout probe of the fp32 32x32x2 MFMA builtin: d[32][32] = a[32][2] @ b[2][32] */
 int ptk_mfma_probe(const float *a, const float *b, float *d, void *s);

@@ -1186,27 +1186,39 @@ extern "C" int ptk_leaky(const float *a, float *y, int64_t n, float alpha, void 
 // One workgroup produces TAIL_OUT consecutive samples; it recomputes the ~TAIL_OUT/16 + 5 frames
 // per band it needs (in LDS), so the whole tail is a single pass over p with no intermediates.
 #define TAIL_OUT 512
-// phase 4 maps thread t of a block to output o0 + t: one output per thread, TAIL_OUT threads.
-// 512 measured best: 256 recomputes more frames per output (26 for 16), 1024 leaves most CUs idle
-// at batch 1 (57 blocks for one T = 226 request)
+// 512 samples per workgroup measured best: 256 recomputes more frames per output (26 for 16),
+// 1024 leaves most CUs idle at batch 1 (57 blocks for one T = 226 request)
+#define TAIL_THREADS 512
 #define TAIL_NY (TAIL_OUT / 4 + 18)
 #define TAIL_NT (TAIL_NY / 4 + 6)
+#define TAIL_KP 12   // a frame's 9 spectrum values padded to 12: three aligned float4 reads
 
-__global__ void __launch_bounds__(TAIL_OUT) tail_kernel(const float *__restrict__ p, long long ldp,
-                                                    long long bsp, long long L,
-                                                    float *__restrict__ wav, long long bsw,
-                                                    const float *__restrict__ cst, ptk_emit em) {
+__global__ void __launch_bounds__(TAIL_THREADS) tail_kernel(const float *__restrict__ p, long long ldp,
+                                                        long long bsp, long long L,
+                                                        float *__restrict__ wav, long long bsw,
+                                                        const float *__restrict__ cst, ptk_emit em) {
   // samples of this item that are kept; a block entirely outside them does no work
   const long long e_lo = blockIdx.y == 0 ? em.lo_first : em.lo;
   const long long e_hi = blockIdx.y + 1 == gridDim.y ? em.hi_last : em.hi;
   if ((long long) blockIdx.x * TAIL_OUT >= e_hi || ((long long) blockIdx.x + 1) * TAIL_OUT <= e_lo) return;
-  __shared__ float s_c[PTK_TAIL_NCONST];
-  __shared__ float s_re[4][TAIL_NT][9], s_im[4][TAIL_NT][9];
+  __shared__ __align__(16) float s_re[4][TAIL_NT][TAIL_KP];
+  __shared__ __align__(16) float s_im[4][TAIL_NT][TAIL_KP];
   __shared__ float s_fr[4][TAIL_NT][16];
   __shared__ float s_y[4][TAIL_NY];
-  const int tid = threadIdx.x;
-  for (int i = tid; i < PTK_TAIL_NCONST; i += TAIL_OUT) s_c[i] = cst[i];
-  const float *hann = s_c, *bc = s_c + 16, *bs = s_c + 160, *h = s_c + 304, *hb = s_c + 556;
+  __shared__ float s_hann[16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const float *hann = cst, *bc = cst + 16, *bs = cst + 160, *hp = cst + 304, *hb = cst + 560;
+  if (tid < 16) s_hann[tid] = hann[tid];
+  // the basis column of this thread's phase-2 sample, loaded while phase 1 runs
+  const int n2 = tid & 15, g2 = tid >> 4;
+  float cb[9], sb[9];
+#pragma unroll
+  for (int k = 0; k < 9; k++) {
+    cb[k] = bc[k * 16 + n2];
+    sb[k] = bs[k * 16 + n2];
+  }
+  const float hn = hann[n2];
   const long long Ly = 4 * (L - 1);
   const long long nout = 4 * Ly;
   const long long o0 = (long long) blockIdx.x * TAIL_OUT;
@@ -1217,77 +1229,127 @@ __global__ void __launch_bounds__(TAIL_OUT) tail_kernel(const float *__restrict_
   const long long i_lo = (o0 - 31) >> 2;
   // frames t needed by ola index j = i + 8 >= i_lo + 8: 4t in [j - 15, j]
   const long long t_lo = (i_lo - 4) >> 2;
-  __syncthreads();
-  // 1) spectra of the needed frames; consecutive threads take consecutive frames of one
-  //    (band, bin) row, so the reads of p are coalesced
-  for (int e = tid; e < 4 * 9 * TAIL_NT; e += TAIL_OUT) {
-    const int tt = e % TAIL_NT, bk = e / TAIL_NT, b = bk / 9, k = bk % 9;
-    const long long t = t_lo + tt;
-    float re = 0.0f, im = 0.0f;
-    if (t >= 0 && t < L) {
-      const float mag = expf(p[(long long) (b * 18 + k) * ldp + t]);
-      const float ph = sinf(p[(long long) (b * 18 + 9 + k) * ldp + t]) * 3.1415927f;
-      float sn, cs;
-      sincosf(ph, &sn, &cs);
-      re = mag * cs;
-      im = mag * sn;
-    }
-    s_re[b][tt][k] = re;
-    s_im[b][tt][k] = im;
-  }
-  __syncthreads();
-  // 2) windowed frames (irfft through the basis)
-  for (int e = tid; e < 4 * TAIL_NT * 16; e += TAIL_OUT) {
-    const int b = e / (TAIL_NT * 16), rem = e % (TAIL_NT * 16), tt = rem / 16, n = rem % 16;
-    float fr = 0.0f, fi = 0.0f;
+  // 1) spectra of the needed frames: wave w takes rows (band, bin) w, w + 8, ...; its lanes take
+  //    consecutive frames, so the reads of p are coalesced.  All of a lane's reads are issued
+  //    before any of them is used.
+  constexpr int NROW = (36 + TAIL_THREADS / 64 - 1) / (TAIL_THREADS / 64);
+  const long long t1 = t_lo + lane;
+  const bool tin = lane < TAIL_NT && t1 >= 0 && t1 < L;
+  float lm[NROW], lph[NROW];
 #pragma unroll
-    for (int k = 0; k < 9; k++) {
-      fr += s_re[b][tt][k] * bc[k * 16 + n];
-      fi += s_im[b][tt][k] * bs[k * 16 + n];
+  for (int it = 0; it < NROW; it++) {
+    const int row = wv + it * (TAIL_THREADS / 64);
+    const int b = row / 9, k = row - 9 * b;
+    lm[it] = lph[it] = 0.0f;
+    if (row < 36 && tin) {
+      lm[it] = p[(long long) (b * 18 + k) * ldp + t1];
+      lph[it] = p[(long long) (b * 18 + 9 + k) * ldp + t1];
     }
-    s_fr[b][tt][n] = (fr + fi) * hann[n];
   }
-  __syncthreads();
-  // 3) overlap-add, window-sum normalisation, [8:-8] trim
-  for (int e = tid; e < 4 * TAIL_NY; e += TAIL_OUT) {
-    const int b = e / TAIL_NY, ii = e % TAIL_NY;
-    const long long i = i_lo + ii;
-    float yv = 0.0f;
-    if (i >= 0 && i < Ly) {
-      const long long j = i + 8;
-      const int r = (int) (j & 3);
-      const long long qq = j >> 2;
-      float ola = 0.0f, ws = 0.0f;
-      for (int jt = 0; jt < 4; jt++) {   // tap jt: frame t = qq - jt, sample n = r + 4*jt
-        const long long t = qq - jt;
-        if (t < 0 || t >= L) continue;
-        const int n = r + 4 * jt;
-        ola += s_fr[b][(int) (t - t_lo)][n];
-        ws += hann[n] * hann[n];
+#pragma unroll
+  for (int it = 0; it < NROW; it++) {
+    const int row = wv + it * (TAIL_THREADS / 64);
+    const int b = row / 9, k = row - 9 * b;
+    if (row < 36 && lane < TAIL_NT) {
+      float re = 0.0f, im = 0.0f;
+      if (tin) {
+        // the hardware transcendentals: v_exp_f32 is 2^x, v_sin_f32 / v_cos_f32 take revolutions
+        // (sin(2 pi x)).  The phase pi * sin(p) in revolutions is sin(p) / 2, within [-1/2, 1/2],
+        // so no range reduction is needed; p itself is a conv output of modest size.
+        const float mag = __builtin_amdgcn_exp2f(lm[it] * 1.44269504f);
+        const float rev = 0.5f * __builtin_amdgcn_sinf(lph[it] * 0.159154943f);
+        re = mag * __builtin_amdgcn_cosf(rev);
+        im = mag * __builtin_amdgcn_sinf(rev);
       }
-      const float eps = 1e-9f;
-      yv = ola / (ws > eps ? ws : eps);
+      s_re[b][lane][k] = re;
+      s_im[b][lane][k] = im;
     }
-    s_y[b][ii] = yv;
   }
   __syncthreads();
-  // 4) PQMF synthesis: zero-insert x4 (gain 4), 63-tap FIR per band, sum of bands
-  // o0 is a multiple of 4, so tap m of output o reads y index (o + m - 31) >> 2, which is
-  // s_y[b][((tid + m - 31) >> 2) + 8]: the same slots for every block.  y outside [0, Ly) is
-  // stored as 0 above, so taps there add 0 and need no range test.
-  const long long o = o0 + tid;
-  if (o >= nout) return;
-  float acc = 0.0f;
-  const int m0 = (31 - tid) & 3;                 // first tap with (o + m - 31) % 4 == 0
-  const int y0 = ((tid + m0 - 31) >> 2) + 8;     // its s_y slot; tap m0 + 4j reads y0 + j
-  for (int b = 0; b < 4; b++) {
+  // 2) windowed frames (irfft through the basis): thread (n, g) owns sample n of frames g, g + 32,
+  //    with the basis column of n and hann[n] in registers; the 16 threads of a frame read its
+  //    spectrum together (broadcast reads)
+  {
+    const int n = n2;
+    constexpr int NFR = 4 * TAIL_NT, NG = TAIL_THREADS / 16;
 #pragma unroll
-    for (int j = 0; j < 16; j++) {
-      const int m = m0 + 4 * j;
-      if (m < 63) acc += h[b * 63 + m] * (4.0f * s_y[b][y0 + j]);
+    for (int it = 0; it < (NFR + NG - 1) / NG; it++) {
+      const int f = g2 + it * NG;   // frame f of the block: band f / TAIL_NT, frame f % TAIL_NT
+      if (f < NFR) {
+        const int b = f / TAIL_NT, tt = f - b * TAIL_NT;
+        const float4 *re4 = reinterpret_cast<const float4 *>(s_re[b][tt]);
+        const float4 *im4 = reinterpret_cast<const float4 *>(s_im[b][tt]);
+        const float4 r0 = re4[0], r1 = re4[1], r2 = re4[2];
+        const float4 i0 = im4[0], i1 = im4[1], i2 = im4[2];
+        const float re[9] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w, r2.x};
+        const float im[9] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w, i2.x};
+        float fr = 0.0f, fi = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 9; k++) {
+          fr += re[k] * cb[k];
+          fi += im[k] * sb[k];
+        }
+        s_fr[b][tt][n] = (fr + fi) * hn;
+      }
     }
   }
-  if (o >= e_lo && o < e_hi) wav[o] = acc + hb[0];
+  __syncthreads();
+  // 3) overlap-add, window-sum normalisation, [8:-8] trim (all bands' y over all threads)
+#pragma unroll
+  for (int it = 0; it < (4 * TAIL_NY + TAIL_THREADS - 1) / TAIL_THREADS; it++) {
+    const int e = tid + it * TAIL_THREADS;
+    if (e < 4 * TAIL_NY) {
+      const int b = e / TAIL_NY, ii = e - b * TAIL_NY;
+      const long long i = i_lo + ii;
+      float yv = 0.0f;
+      if (i >= 0 && i < Ly) {
+        const long long j = i + 8;
+        const int r = (int) (j & 3);
+        const long long qq = j >> 2;
+        float ola = 0.0f, ws = 0.0f;
+#pragma unroll
+        for (int jt = 0; jt < 4; jt++) {   // tap jt: frame t = qq - jt, sample n = r + 4*jt
+          const long long t = qq - jt;
+          if (t < 0 || t >= L) continue;
+          const int n = r + 4 * jt;
+          ola += s_fr[b][(int) (t - t_lo)][n];
+          ws += s_hann[n] * s_hann[n];
+        }
+        const float eps = 1e-9f;
+        yv = ola / (ws > eps ? ws : eps);
+      }
+      s_y[b][ii] = yv;
+    }
+  }
+  __syncthreads();
+  // 4) PQMF synthesis: zero-insert x4 (gain 4), 63-tap FIR per band, sum of bands.  Thread u
+  // makes samples o0 + 4u + r, r = 0..3: sample r uses the taps m = (3 - r) + 4j, and every one of
+  // the four reads the same y slots u + 1 + j (o0 is a multiple of 4), so the 16 y values of a band
+  // are read once for four samples, and the taps are the same for every thread (scalar loads).
+  // y outside [0, Ly) is stored as 0 above, so taps there add 0 and need no range test.
+  const int u = tid;
+  if (u >= TAIL_OUT / 4) return;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int b = 0; b < 4; b++) {
+    float y[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) y[j] = 4.0f * s_y[b][u + 1 + j];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        if (3 - r + 4 * j < 63) acc[r] += hp[(b * 4 + r) * 16 + j] * y[j];
+      }
+    }
+  }
+  const long long ob = o0 + 4 * u;
+  const float bias = hb[0];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const long long o = ob + r;
+    if (o < nout && o >= e_lo && o < e_hi) wav[o] = acc[r] + bias;
+  }
 }
 
 extern "C" int ptk_tail_batched(const float *p, int64_t ldp, int64_t bsp, int64_t L, float *wav,
@@ -1302,7 +1364,7 @@ extern "C" int ptk_tail_batched(const float *p, int64_t ldp, int64_t bsp, int64_
   const ptk_emit all = {0, 0, nout, nout};
   const ptk_emit em = emit ? *emit : all;
   const unsigned blocks = (unsigned) ((nout + TAIL_OUT - 1) / TAIL_OUT);
-  hipLaunchKernelGGL(tail_kernel, dim3(blocks, (unsigned) batch), dim3(TAIL_OUT), 0, (hipStream_t) s, p,
+  hipLaunchKernelGGL(tail_kernel, dim3(blocks, (unsigned) batch), dim3(TAIL_THREADS), 0, (hipStream_t) s, p,
                      (long long) ldp, (long long) bsp, (long long) L, wav, (long long) bsw, consts, em);
   HCHK(hipGetLastError());
   return 0;
