@@ -1203,11 +1203,10 @@ __global__ void __launch_bounds__(TAIL_THREADS) tail_kernel(const float *__restr
   if ((long long) blockIdx.x * TAIL_OUT >= e_hi || ((long long) blockIdx.x + 1) * TAIL_OUT <= e_lo) return;
   __shared__ __align__(16) float s_re[4][TAIL_NT][TAIL_KP];
   __shared__ __align__(16) float s_im[4][TAIL_NT][TAIL_KP];
-  __shared__ float s_fr[4][TAIL_NT][16];
+  __shared__ __align__(16) float s_fr[4][TAIL_NT][16];
   __shared__ float s_y[4][TAIL_NY];
   __shared__ float s_hann[16];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tid = threadIdx.x;
   const float *hann = cst, *bc = cst + 16, *bs = cst + 160, *hp = cst + 304, *hb = cst + 560;
   if (tid < 16) s_hann[tid] = hann[tid];
   // the basis column of this thread's phase-2 sample, loaded while phase 1 runs
@@ -1229,30 +1228,30 @@ __global__ void __launch_bounds__(TAIL_THREADS) tail_kernel(const float *__restr
   const long long i_lo = (o0 - 31) >> 2;
   // frames t needed by ola index j = i + 8 >= i_lo + 8: 4t in [j - 15, j]
   const long long t_lo = (i_lo - 4) >> 2;
-  // 1) spectra of the needed frames: wave w takes rows (band, bin) w, w + 8, ...; its lanes take
-  //    consecutive frames, so the reads of p are coalesced.  All of a lane's reads are issued
-  //    before any of them is used.
-  constexpr int NROW = (36 + TAIL_THREADS / 64 - 1) / (TAIL_THREADS / 64);
-  const long long t1 = t_lo + lane;
-  const bool tin = lane < TAIL_NT && t1 >= 0 && t1 < L;
-  float lm[NROW], lph[NROW];
+  // 1) spectra of the needed frames: element e = row * TAIL_NT + frame over all threads (row =
+  //    band * 9 + bin), so consecutive threads read consecutive frames of a row (coalesced).  All
+  //    of a thread's reads are issued before any of them is used.
+  constexpr int NSP = 36 * TAIL_NT, NIT1 = (NSP + TAIL_THREADS - 1) / TAIL_THREADS;
+  float lm[NIT1], lph[NIT1];
 #pragma unroll
-  for (int it = 0; it < NROW; it++) {
-    const int row = wv + it * (TAIL_THREADS / 64);
-    const int b = row / 9, k = row - 9 * b;
+  for (int it = 0; it < NIT1; it++) {
+    const int e = tid + it * TAIL_THREADS;
+    const int row = e / TAIL_NT, tt = e - row * TAIL_NT, b = row / 9, k = row - 9 * b;
+    const long long t = t_lo + tt;
     lm[it] = lph[it] = 0.0f;
-    if (row < 36 && tin) {
-      lm[it] = p[(long long) (b * 18 + k) * ldp + t1];
-      lph[it] = p[(long long) (b * 18 + 9 + k) * ldp + t1];
+    if (e < NSP && t >= 0 && t < L) {
+      lm[it] = p[(long long) (b * 18 + k) * ldp + t];
+      lph[it] = p[(long long) (b * 18 + 9 + k) * ldp + t];
     }
   }
 #pragma unroll
-  for (int it = 0; it < NROW; it++) {
-    const int row = wv + it * (TAIL_THREADS / 64);
-    const int b = row / 9, k = row - 9 * b;
-    if (row < 36 && lane < TAIL_NT) {
+  for (int it = 0; it < NIT1; it++) {
+    const int e = tid + it * TAIL_THREADS;
+    const int row = e / TAIL_NT, tt = e - row * TAIL_NT, b = row / 9, k = row - 9 * b;
+    const long long t = t_lo + tt;
+    if (e < NSP) {
       float re = 0.0f, im = 0.0f;
-      if (tin) {
+      if (t >= 0 && t < L) {
         // the hardware transcendentals: v_exp_f32 is 2^x, v_sin_f32 / v_cos_f32 take revolutions
         // (sin(2 pi x)).  The phase pi * sin(p) in revolutions is sin(p) / 2, within [-1/2, 1/2],
         // so no range reduction is needed; p itself is a conv output of modest size.
@@ -1261,8 +1260,8 @@ __global__ void __launch_bounds__(TAIL_THREADS) tail_kernel(const float *__restr
         re = mag * __builtin_amdgcn_cosf(rev);
         im = mag * __builtin_amdgcn_sinf(rev);
       }
-      s_re[b][lane][k] = re;
-      s_im[b][lane][k] = im;
+      s_re[b][tt][k] = re;
+      s_im[b][tt][k] = im;
     }
   }
   __syncthreads();
