@@ -481,11 +481,13 @@ def main():
     f1()
     ms = timer.time(f1, 50)
     cfg["config1_conv_tflops"] = round(2 * 512 * 192 * 7 * 226 / (ms * 1e-3) / 1e12, 3)
+    cfg["config1_frac"] = round(cfg["config1_conv_tflops"] / MFMA_F32_PEAK, 4)
     dx0 = pkg.DevBuf(256 * 904)
     f2 = lambda: lib.ptd_layer(ctx.ptr, model.ptr, 1, dh.ptr, 226, 1, dx0.ptr, 0.1, 0.0)  # noqa: E731
     f2()
     ms = timer.time(f2, 50)
     cfg["config2_convT_tflops"] = round(2 * 256 * 512 * 4 * 904 / (ms * 1e-3) / 1e12, 3)
+    cfg["config2_frac"] = round(cfg["config2_convT_tflops"] / MFMA_F32_PEAK, 4)
     for stage, (C_, T) in enumerate([(256, 904), (128, 3616)]):
         x = pkg.DevBuf.of(ctx, np.random.default_rng(5).standard_normal((C_, T)).astype(np.float32))
         y = pkg.DevBuf(C_ * T)
@@ -494,6 +496,7 @@ def main():
         ms = timer.time(f3, 20)
         # 3 dilations x (c1 + c2) x branches K 3 + 7 + 11 = 126 tap-weighted convs of C x C
         cfg[f"config3_mrf{C_}_tflops"] = round(2 * C_ * C_ * T * 126 / (ms * 1e-3) / 1e12, 3)
+        cfg[f"config3_mrf{C_}_frac"] = round(cfg[f"config3_mrf{C_}_tflops"] / MFMA_F32_PEAK, 4)
         x.free()
         y.free()
     # config 4: one request, one stream
@@ -680,6 +683,8 @@ def main():
                         "one shared weight set",
             "request_frames": Ts, "longform_frames": T_long, "audio_s_per_step": round(audio_step, 4),
             "audio_s_8_requests": round(audio8, 4), "parallelism": "1 GPU, 9 streams",
+            "io": "latents and waveforms device-resident in the timed step (uploaded before it, "
+                  "read back after it)",
         },
         "roofline": {
             "kernel": "conv_mfma_kernel (MRF-256 grouped launch: 3 branch convs K 3/7/11, C 256, T 904)",

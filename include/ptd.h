@@ -241,6 +241,9 @@ float ptd_event_elapsed_ms(void *e0, void *e1); /* waits for e1; negative on err
 /* fp32 32x32x2 MFMA lane-layout probe (test hook): d[32][32] = a[32][2] @ b[2][32], host
  * buffers, synchronous on the context's stream. */
 int ptd_mfma_probe(pt_ctx *c, const float *a, const float *b, float *d);
+/* the same for the fp32 16x16x4 MFMA builtin the 16-row conv tiles use: a[16][4], b[4][16] ->
+ * d[16][16] (host buffers) */
+int ptd_mfma16_probe(pt_ctx *c, const float *a, const float *b, float *d);
 /* closed-form part of the tail table as the device uses it (host copy, PTD_TAIL_NCONST floats):
  * periodic Hann(16), irfft basis cos rows (9 x 16), -sin rows (9 x 16) */
 #define PTD_TAIL_NCONST (16 + 144 + 144)

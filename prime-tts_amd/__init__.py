@@ -102,6 +102,7 @@ _SIGS = {
     "ptd_event_record": (C.c_int, [VP, VP]),
     "ptd_event_elapsed_ms": (C.c_float, [VP, VP]),
     "ptd_mfma_probe": (C.c_int, [VP, F, F, F]),
+    "ptd_mfma16_probe": (C.c_int, [VP, F, F, F]),
     "ptd_tail_constants": (None, [F]),
     "ptd_ctx_layout": (C.c_int, [C.POINTER(C.c_long), C.c_int]),
 }

@@ -57,6 +57,7 @@ static layer_geo dec_geo(int i) {
 struct ptd_model {
   void *slab;                      /* relaid weights, biases, tail constants */
   const float *wr[PTD_DEC_NLAYER]; /* MFMA layout [Mp/32][K][cinp/8][64][4] */
+  const float *wr16[PTD_DEC_NLAYER]; /* for 16-row tiles [Mp/16][K][cinp/8][64][2] */
   const float *b[PTD_DEC_NLAYER];
   const float *consts;             /* the tail's table: hann, basis_c, basis_s, final conv */
   layer_geo g[PTD_DEC_NLAYER];
@@ -116,7 +117,7 @@ ptd_model *ptdi_model_build(pt_ctx *c, const void *const *w, const int *wisz, co
   ptd_model *m = calloc(1, sizeof *m);
   if (!m) return NULL;
   size_t total = 0, packed_max = 0, half_max = 0;
-  size_t off_w[PTD_DEC_NLAYER], off_b[PTD_DEC_NLAYER];
+  size_t off_w[PTD_DEC_NLAYER], off_w16[PTD_DEC_NLAYER], off_b[PTD_DEC_NLAYER];
   int64_t wn[PTD_DEC_NLAYER];
   const int last = PTD_DEC_NLAYER - 1;
   if (!w[last] || (wisz && wisz[last] != 4)) {
@@ -140,6 +141,8 @@ ptd_model *ptdi_model_build(pt_ctx *c, const void *const *w, const int *wisz, co
     if (isz == 2 && (size_t) wn[i] * 2 > half_max) half_max = (size_t) wn[i] * 2;
     off_w[i] = total;
     total += al256(ptk_relayout_floats(M, K, g.cin) * sizeof(float));
+    off_w16[i] = total;
+    total += al256(ptk_relayout16_floats(M, K, g.cin) * sizeof(float));
     off_b[i] = total;
     total += al256((size_t) g.cout * sizeof(float));
   }
@@ -166,10 +169,12 @@ ptd_model *ptdi_model_build(pt_ctx *c, const void *const *w, const int *wisz, co
         : (ptk_h2d_async(tmp16, w[i], (size_t) wn[i] * 2, c->g_stream) ||
            ptk_h2f((float *) tmp, (const uint16_t *) tmp16, wn[i], c->g_stream));
     if (up || ptk_relayout((float *) (base + off_w[i]), tmp, M, K, g.cin, c->g_stream) ||
+        ptk_relayout16((float *) (base + off_w16[i]), tmp, M, K, g.cin, c->g_stream) ||
         ptk_h2d_async(base + off_b[i], b[i], (size_t) g.cout * sizeof(float), c->g_stream) ||
         ptk_stream_sync(c->g_stream))
       goto fail;
     m->wr[i] = (const float *) (base + off_w[i]);
+    m->wr16[i] = (const float *) (base + off_w16[i]);
     m->b[i] = (const float *) (base + off_b[i]);
   }
   if (ptk_h2d_async(base + off_c, consts, sizeof consts, c->g_stream) || ptk_stream_sync(c->g_stream))
@@ -205,6 +210,7 @@ static void conv_layer_desc(ptk_conv_desc *d, const ptd_model *m, int i, const f
   const int c4 = (g.cout + 3) / 4 * 4;
   ptdi_conv_desc(d, x, ldx, (int64_t) g.cin * ldx, T, g.cin, m->wr[i], m->b[i], g.cout, g.K, 1,
                  g.sd, g.pad, c4, y, ldy, (int64_t) c4 * ldy, T, batch);
+  d->w16 = m->wr16[i];
 }
 
 static void epi_push(ptk_conv_desc *d, int op, float a, const float *t, int64_t ldt, int64_t bst) {
@@ -329,10 +335,12 @@ static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t ld
   /* conv_pre + LeakyReLU */
   ptdi_conv_desc(&d, z, ldz, bsz, T, 192, m->wr[0], m->b[0], 512, 7, 1, 1, 3, 512, h, T, 512 * T, T,
                  batch);
+  d.w16 = m->wr16[0];
   epi_push(&d, PTK_EPI_LEAKY, 0.1f, NULL, 0, 0);
   if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
   /* ups.0 */
   ptdi_convT_desc(&d, h, T, 512 * T, T, 512, m->wr[1], m->b[1], 256, 4, 6, 16, x0, T1, 256 * T1, batch);
+  d.w16 = m->wr16[1];
   d.y2 = x0L;
   d.a2 = 0.1f;
   if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
@@ -349,6 +357,7 @@ static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t ld
   if (!av0 || ptk_avg3_leaky(o0[0], o0[1], o0[2], av0, (int64_t) batch * 256 * T1, 0.1f, c->g_stream)) goto fail;
   ptdi_convT_desc(&d, av0, T1, 256 * T1, T1, 256, m->wr[20], m->b[20], 128, 4, 6, 16, x1, T2,
                   128 * T2, batch);
+  d.w16 = m->wr16[20];
   d.y2 = x1L;
   d.a2 = 0.1f;
   if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
@@ -362,6 +371,7 @@ static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t ld
   if (!av1 || ptk_avg3_leaky(o1[0], o1[1], o1[2], av1, (int64_t) batch * 128 * T2, 0.01f, c->g_stream)) goto fail;
   ptdi_conv_desc(&d, av1, T2, 128 * T2, L, 128, m->wr[39], m->b[39], 72, 7, 1, 1, 3, 72, p, L,
                  72 * L, L, batch);
+  d.w16 = m->wr16[39];
   d.reflect_l1 = 1;
   if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
   if (ptk_tail_batched(p, L, 72 * L, L, wav, bsw, batch, m->consts, emit, c->g_stream)) goto fail;
@@ -442,6 +452,7 @@ int ptd_layer(pt_ctx *c, const ptd_model *m, int layer, const float *x, int64_t 
     const int64_t Lout = (T - 1) * g.sd - 2 * g.pad + g.K;
     ptdi_convT_desc(&d, x, T, (int64_t) g.cin * T, T, g.cin, m->wr[layer], m->b[layer], g.cout,
                     g.sd, g.pad, g.K, y, Lout, (int64_t) c4 * Lout, batch);
+    d.w16 = m->wr16[layer];
   } else {
     conv_layer_desc(&d, m, layer, x, T, T, batch, y, T);
   }

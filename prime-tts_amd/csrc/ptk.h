@@ -91,6 +91,9 @@ typedef struct {
   int reflect_l1;             /* virtual column 0 reads physical column 1, column c>0 reads c-1 */
   /* weights: relaid [Mp/32][K][cinp/8][64][4] (see ptk_relayout) */
   const float *w;
+  /* optional: the same weights relaid for 16-row tiles [Mp/16][K][cinp/8][64][2]
+     (ptk_relayout16); NULL keeps the launch on 32-row tiles */
+  const float *w16;
   int cinp;
   const float *bias;
   int nbias;
@@ -117,6 +120,9 @@ typedef struct {
 int ptk_conv_cinp(int cin);
 size_t ptk_relayout_floats(int M, int K, int cin);
 int ptk_relayout(float *dst, const float *wp, int M, int K, int cin, void *s);
+/* the copy for 16-row tiles: [Mp/16][K][cinp/8][64][2], Mp = M rounded up to 16 */
+size_t ptk_relayout16_floats(int M, int K, int cin);
+int ptk_relayout16(float *dst, const float *wp, int M, int K, int cin, void *s);
 /* fp16 -> fp32 expansion of n items (bit-exact: subnormals keep their value, inf / NaN keep sign
  * and payload, nothing is quieted) */
 int ptk_h2f(float *dst, const uint16_t *src, int64_t n, void *s);
@@ -167,6 +173,8 @@ int ptk_tail_batched(const float *p, int64_t ldp, int64_t bsp, int64_t L, float 
 
 /* lane-layout probe of the fp32 32x32x2 MFMA builtin: d[32][32] = a[32][2] @ b[2][32] */
 int ptk_mfma_probe(const float *a, const float *b, float *d, void *s);
+/* and of the fp32 16x16x4 one: d[16][16] = a[16][4] @ b[4][16] */
+int ptk_mfma16_probe(const float *a, const float *b, float *d, void *s);
 
 #ifdef __cplusplus
 }

@@ -2,7 +2,8 @@
 // layer (ptk.h) through which the C host code reaches them.
 //
 // Wide Conv1d / ConvTranspose1d run as one implicit GEMM on the fp32 matrix cores
-// (v_mfma_f32_32x32x2_f32): GEMM rows are output channels (convT: phase rows r*C4 + co, the
+// (v_mfma_f32_32x32x2_f32, or v_mfma_f32_16x16x4_f32 for 16-row tiles when one batch item's grid
+// is too small to fill the chip): GEMM rows are output channels (convT: phase rows r*C4 + co, the
 // reference's packed phase layout), columns are output positions, the reduction runs over
 // (tap, input channel).  im2col never exists: each wave stages a window of input columns per
 // channel chunk in LDS and reads it K times at the K tap shifts.  The four waves of a workgroup
@@ -24,6 +25,7 @@
 #include "ptk.h"
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------------------ error handling
 static thread_local char g_err[512];
@@ -305,6 +307,47 @@ extern "C" int ptk_relayout(float *dst, const float *wp, int M, int K, int cin, 
   return 0;
 }
 
+// The same weights for 16-row tiles on v_mfma_f32_16x16x4_f32: [Mp/16][K][cinp/8][64][2] (Mp = M
+// rounded up to 16).  Lane l = 16*kq + r holds W[mb*16 + r][k][chunk*8 + 4*s + kq], s = 0, 1: its
+// A operands (row r, reduction index kq) of the two MFMAs that consume channels 4s .. 4s + 3 of
+// the chunk.  One 8-byte load per lane feeds both, and a wave's (tap, chunk) slice is 512
+// contiguous bytes.
+extern "C" size_t ptk_relayout16_floats(int M, int K, int cin) {
+  const size_t Mp = (size_t) (M + 15) / 16 * 16;
+  return Mp * (size_t) K * (size_t) ptk_conv_cinp(cin);
+}
+
+__global__ void relayout16_kernel(float *__restrict__ dst, const float *__restrict__ wp, int M,
+                                  int K, int cin, int cinp, long long total) {
+  long long i = (long long) blockIdx.x * blockDim.x + threadIdx.x;
+  const long long st = (long long) gridDim.x * blockDim.x;
+  const int nchunk = cinp / CONV_CK;
+  for (; i < total; i += st) {
+    const int s = (int) (i & 1);
+    const int lane = (int) ((i >> 1) & 63);
+    long long r = i >> 7;
+    const int chunk = (int) (r % nchunk);
+    r /= nchunk;
+    const int k = (int) (r % K);
+    const int mb = (int) (r / K);
+    const int m = mb * 16 + (lane & 15);
+    const int ci = chunk * CONV_CK + 4 * s + (lane >> 4);
+    float v = 0.0f;
+    if (m < M && ci < cin) v = wp[(((long long) (m >> 2) * K + k) * cin + ci) * 4 + (m & 3)];
+    dst[i] = v;
+  }
+}
+
+extern "C" int ptk_relayout16(float *dst, const float *wp, int M, int K, int cin, void *s) {
+  const long long total = (long long) ptk_relayout16_floats(M, K, cin);
+  long long blocks = (total + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(relayout16_kernel, dim3((unsigned) blocks), dim3(256), 0, (hipStream_t) s,
+                     dst, wp, M, K, cin, ptk_conv_cinp(cin), total);
+  HCHK(hipGetLastError());
+  return 0;
+}
+
 // ------------------------------------------------------------------------------ fp16 expansion
 // binary16 -> binary32 by its bit fields.  Every binary16 value is exact in binary32: normals
 // rebias the exponent (15 -> 127), subnormals m * 2^-24 renormalise around their leading one,
@@ -380,6 +423,25 @@ template <int NB> struct WinGeo {
   static constexpr int XWMAX = 64 * NJ;
 };
 
+// 16-row tiles (RB = 16) keep the same window but store it as four planes q = 0..3 of float2
+// columns: plane q, column c = channels q, 4 + q, the B operands (reduction index q) of the two
+// 16x16x4 MFMAs of a chunk.  A quarter-wave reads 16 consecutive float2 of one plane per tap and
+// column block; planes are XWMAX + 16 float2 apart, so the two quarter-waves served together
+// fall on different banks.
+//
+// LDS of one workgroup: per wave its staging area, the partial-sum area (the staging area itself
+// when the partial sums fit in it), then the block's RB bias values.
+template <int NB, int RB> struct LdsGeo {
+  static constexpr int XWMAX = WinGeo<NB>::XWMAX;
+  static constexpr int PS = RB == 32 ? XWMAX : XWMAX + 16;   // plane stride (float4 / float2)
+  static constexpr int STG = 8 * PS;                         // staging floats per wave
+  static constexpr int NV = RB / 2;                          // accumulators per lane and column block
+  static constexpr int RED = NB * NV * 64;                   // partial-sum floats per wave
+  static constexpr bool OWN_RED = RED <= STG;
+  static constexpr int BIAS = CONV_WAVES * (STG > RED ? STG : RED);
+  static constexpr size_t BYTES = (size_t) (BIAS + RB) * sizeof(float);
+};
+
 // word 3 of a raw buffer resource on gfx9-family parts (gfx950): 32-bit data, range checked
 #define PTK_BUF_WORD3 0x00020000
 // an offset past every buffer: the load returns 0 (buffer range checking)
@@ -399,15 +461,19 @@ __device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, unsigned vof
 }
 
 // One workgroup = 4 waves.  The waves form 4/S column groups of S waves; the S waves of a group
-// compute the same 32-row x 32*NB-column output block over disjoint quarters/halves of the input
+// compute the same RB-row x 32*NB-column output block over disjoint quarters/halves of the input
 // channels (S = 1: each wave its own block over all channels) and are reduced through LDS in wave
 // order (deterministic).  KT > 0: every problem of the group has K <= KT and the whole next chunk's
-// A operands (KT float4 per lane) are prefetched while the current chunk runs; KT == 0: any K, A
-// loaded per tap.  IN: input transform (PTK_IN_*).
-template <int KT, int NB, int IN>
+// A operands (KT float4 / float2 per lane) are prefetched while the current chunk runs; KT == 0:
+// any K, A loaded per tap.  IN: input transform (PTK_IN_*).  RB: rows per tile, 32 (32x32x2 MFMA,
+// weights from d.w) or 16 (16x16x4 MFMA on two 16-column blocks, weights from d.w16).
+template <int KT, int NB, int IN, int RB>
 __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   extern __shared__ float smem[];
+  static_assert(RB == 32 || (RB == 16 && NB == 1), "16-row tiles are built for one column block");
   constexpr int NJ = WinGeo<NB>::NJ, XWMAX = WinGeo<NB>::XWMAX;
+  using Geo = LdsGeo<NB, RB>;
+  constexpr int PS = Geo::PS, NV = Geo::NV;
   int bid = blockIdx.x;
   int p = 0;
 #pragma unroll
@@ -455,27 +521,29 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   // the wave-based buffer resources would be treated as divergent)
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ks = w % S, cg = w / S;             // channel split index, column group
-  // The block's 32 bias values go to LDS once, past the staging / reduction area, so that the
+  // The block's RB bias values go to LDS once, past the staging / reduction area, so that the
   // epilogue adds them from LDS: a global load per element there, placed after the previous
   // element's stores, would wait out a whole memory latency each time.
-  constexpr int BIAS_LDS = (CONV_WAVES * CONV_CK * XWMAX > CONV_WAVES * NB * 16 * 64)
-                               ? CONV_WAVES * CONV_CK * XWMAX : CONV_WAVES * NB * 16 * 64;
-  float *bsh = smem + BIAS_LDS;
-  if (w == 0 && lane < 32) {
-    const int m = mb * 32 + lane;
+  float *bsh = smem + Geo::BIAS;
+  if (w == 0 && lane < RB) {
+    const int m = mb * RB + lane;
     int co = m;
     if (d.C4 != d.M) co = m - (m / d.C4) * d.C4;
     bsh[lane] = (d.bias != nullptr && m < d.M && co < d.nbias) ? d.bias[co] : 0.0f;
   }
-  const int half = lane >> 5;     // which of the two reduction rows this lane feeds
+  const int half = lane >> 5;     // RB = 32: which of the two reduction rows this lane feeds
   const int l32 = lane & 31;
+  const int quad = lane >> 4;     // RB = 16: the reduction index (and row group) of this lane
+  const int l16 = lane & 15;
   const long long q0 = d.q0 + ((long long) tn * G + cg) * (32 * NB);
   const int kd = (K - 1) * dil;
   const int dmin = kd < 0 ? kd : 0;
   const int XW = (32 * NB - 1) * st + (kd < 0 ? -kd : kd) + 1;
   const long long cmin = q0 * st + dmin - d.shift;
   const int chunk0 = ks * nch;
-  float4 *xs = reinterpret_cast<float4 *>(smem) + w * (2 * XWMAX);   // [h][column] float4
+  float *xsw = smem + w * Geo::STG;   // this wave's staging planes
+  float4 *xs = reinterpret_cast<float4 *>(xsw);    // RB = 32: [h][column] float4
+  float2 *xs2 = reinterpret_cast<float2 *>(xsw);   // RB = 16: [q][column] float2
 
   // Window columns this lane stages, fixed for the wave: byte offset in the row, or an offset the
   // buffer range check turns into 0 (columns outside [0, lim), past the window).  The row offset
@@ -531,39 +599,75 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
           for (int r = 0; r < CONV_CK; r++) v[r] = r < nlive ? v[r] : 0.0f;
         }
       }
-      xs[lane + 64 * jj] = make_float4(v[0], v[2], v[4], v[6]);
-      xs[XWMAX + lane + 64 * jj] = make_float4(v[1], v[3], v[5], v[7]);
+      if constexpr (RB == 32) {
+        xs[lane + 64 * jj] = make_float4(v[0], v[2], v[4], v[6]);
+        xs[XWMAX + lane + 64 * jj] = make_float4(v[1], v[3], v[5], v[7]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; q++) xs2[q * PS + lane + 64 * jj] = make_float2(v[q], v[4 + q]);
+      }
     }
   };
 
-  f32x16 acc[NB];
+  // accumulators: RB = 32, one 32x32 block per column block (16 values per lane); RB = 16, two
+  // 16x16 blocks per column block (4 values per lane each)
+  using AccT = std::conditional_t<RB == 32, f32x16, f32x4>;
+  constexpr int NCB = RB == 32 ? 1 : 2;
+  AccT acc[NB][NCB];
 #pragma unroll
   for (int nb = 0; nb < NB; nb++)
 #pragma unroll
-    for (int v = 0; v < 16; v++) acc[nb][v] = 0.0f;
-
-  // A operands: float4 ((mb*K + k)*nchunk + chunk)*64 + lane of the relaid weights, read through
-  // a buffer resource based at this wave's first chunk: the lane offset is fixed and the
-  // (tap, chunk) offset is wave-uniform, so a load costs no vector address arithmetic
-  const float4 *wbase = reinterpret_cast<const float4 *>(d.w) + ((long long) mb * K * nchunk + chunk0) * 64;
-  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-      (void *) wbase, (short) 0, (int) ((unsigned) K * (unsigned) nchunk * 1024u), PTK_BUF_WORD3);
-  const unsigned wlane = (unsigned) lane * 16u;
-  const int wtap = nchunk * 1024;  // bytes between taps
-  auto wa = [&](int k, int j) {
-    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rw, wlane, k * wtap + j * 1024, 0));
-  };
-  const int lbase = half * XWMAX + l32 * st - dmin;   // float4 index of tap 0, column block 0
-
-  auto mfma4 = [&](const float4 a, const float4 *xr) {
+    for (int cb = 0; cb < NCB; cb++)
 #pragma unroll
-    for (int nb = 0; nb < NB; nb++) {
-      const float4 bq = xr[32 * nb * st];
-      acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, bq.x, acc[nb], 0, 0, 0);
-      acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, bq.y, acc[nb], 0, 0, 0);
-      acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, bq.z, acc[nb], 0, 0, 0);
-      acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, bq.w, acc[nb], 0, 0, 0);
+      for (int v = 0; v < NV / NCB; v++) acc[nb][cb][v] = 0.0f;
+
+  // A operands: float4 (RB = 16: float2) ((mb*K + k)*nchunk + chunk)*64 + lane of the relaid
+  // weights, read through a buffer resource based at this wave's first chunk: the lane offset is
+  // fixed and the (tap, chunk) offset is wave-uniform, so a load costs no vector address arithmetic
+  using AT = std::conditional_t<RB == 32, float4, float2>;
+  constexpr int ABYTES = 64 * (int) sizeof(AT);   // one (tap, chunk) slice of a wave
+  const AT *wbase = reinterpret_cast<const AT *>(RB == 32 ? d.w : d.w16) +
+                    ((long long) mb * K * nchunk + chunk0) * 64;
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      (void *) wbase, (short) 0, (int) ((unsigned) K * (unsigned) nchunk * (unsigned) ABYTES),
+      PTK_BUF_WORD3);
+  const unsigned wlane = (unsigned) lane * (unsigned) sizeof(AT);
+  const int wtap = nchunk * ABYTES;  // bytes between taps
+  auto wa = [&](int k, int j) {
+    if constexpr (RB == 32)
+      return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rw, wlane, k * wtap + j * ABYTES, 0));
+    else
+      return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rw, wlane, k * wtap + j * ABYTES, 0));
+  };
+  // staging-plane index of tap 0, column block 0 (float4 for RB = 32, float2 for RB = 16)
+  const int lbase = RB == 32 ? half * XWMAX + l32 * st - dmin : quad * PS + l16 * st - dmin;
+
+  // the MFMAs of one tap: xr points at this lane's B operands of column block 0 (a float4 of
+  // plane h for RB = 32, a float2 of plane quad for RB = 16)
+  auto mfma4 = [&](const AT a, const auto *xr) {
+    if constexpr (RB == 32) {
+#pragma unroll
+      for (int nb = 0; nb < NB; nb++) {
+        const float4 bq = xr[32 * nb * st];
+        acc[nb][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, bq.x, acc[nb][0], 0, 0, 0);
+        acc[nb][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, bq.y, acc[nb][0], 0, 0, 0);
+        acc[nb][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, bq.z, acc[nb][0], 0, 0, 0);
+        acc[nb][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, bq.w, acc[nb][0], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+        for (int cb = 0; cb < 2; cb++) {
+          const float2 bq = xr[(32 * nb + 16 * cb) * st];
+          acc[nb][cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, bq.x, acc[nb][cb], 0, 0, 0);
+          acc[nb][cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, bq.y, acc[nb][cb], 0, 0, 0);
+        }
     }
+  };
+  auto tap = [&](const AT a, int k) {
+    if constexpr (RB == 32) mfma4(a, xs + lbase + k * dil);
+    else mfma4(a, xs2 + lbase + k * dil);
   };
   // The chunk loop, for a compile-time tap count KC (0: runtime K, A operands loaded per tap).
   // Each chunk is straight-line code, so the scheduler can run LDS reads ahead of the MFMAs and
@@ -574,7 +678,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   auto run = [&](auto kc, auto mask, auto nju) {
     constexpr int KC = decltype(kc)::value;
     constexpr int KA = KC > 0 ? KC : 1;
-    float4 acur[KA];
+    AT acur[KA];
     auto chunk = [&](int j, auto with_loads) {
       constexpr bool LD = decltype(with_loads)::value;
       __builtin_amdgcn_wave_barrier();
@@ -589,14 +693,14 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
       if constexpr (KC > 0) {
 #pragma unroll
         for (int k = 0; k < KC; k++) {
-          mfma4(acur[k], xs + lbase + k * dil);
+          tap(acur[k], k);
           if constexpr (LD) {
             acur[k] = wa(k, j + 1);
             PTK_PIN_VMEM();
           }
         }
       } else {
-        for (int k = 0; k < K; k++) mfma4(wa(k, j), xs + lbase + k * dil);
+        for (int k = 0; k < K; k++) tap(wa(k, j), k);
       }
       __builtin_amdgcn_wave_barrier();
     };
@@ -630,10 +734,10 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   }
 
   // Epilogue: the S partial sums of a block are added in wave order through LDS, then bias, the
-  // epilogue chain and one store per output.  Lane (l32, half) of a wave holds, for column block
+  // epilogue chain and one store per output.  RB = 32: lane (l32, half) holds, for column block
   // nb, the 16 values v of column q0 + 32*nb + l32 at rows 8*(v >> 2) + 4*half + (v & 3) of the
-  // 32-row block.  Wave ks of a column group finishes v in [v0, v0 + 16/S): groups g of four
-  // consecutive rows, v = v0 + 4*g + j (v0 is a multiple of 4).
+  // block.  RB = 16: lane (l16, quad) holds 8 values v of column q0 + 32*nb + 16*(v >> 2) + l16 at
+  // rows 4*quad + (v & 3).  Wave ks of a column group finishes v in [v0, v0 + NV/S).
   const long long qend = d.q0 + d.nq;
   const int M = d.M, C4 = d.C4, ys = d.ys, ypad = d.ypad, nepi = d.nepi;
   const long long Lout = d.Lout, ldy = d.ldy;
@@ -646,21 +750,24 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   for (int e = 0; e < nepi; e++)
     if (addt < 0 && d.epi[e].op == PTK_EPI_ADDT) addt = e;
   const long long ldt = addt >= 0 ? d.epi[addt].ldt : 0;
-  const int nv = 16 / S, v0 = ks * nv, ngrp = nv / 4, wg0 = cg * S;
+  const int nv = NV / S, v0 = ks * nv, ngrp = nv / 4, wg0 = cg * S;
+  // row and column of value v inside the block, lane parts included
+  auto vrow = [&](int v) { return RB == 32 ? 8 * (v >> 2) + 4 * half + (v & 3) : 4 * quad + (v & 3); };
+  auto vcol = [&](int nb, int v) { return RB == 32 ? 32 * nb + l32 : 32 * nb + 16 * (v >> 2) + l16; };
 
   // Each wave writes its partial sums over its own staging area, which only it reads, so no wave
-  // waits for the others before writing (a separate region when NB column blocks do not fit).
-  constexpr bool OWN_RED = 16 * NB * 64 <= 8 * XWMAX;
-  auto red_of = [&](int wave) {
-    return OWN_RED ? smem + wave * 8 * XWMAX : smem + wave * NB * 16 * 64;
-  };
+  // waits for the others before writing (a separate region when they do not fit).
+  constexpr bool OWN_RED = Geo::OWN_RED;
+  auto red_of = [&](int wave) { return OWN_RED ? smem + wave * Geo::STG : smem + wave * Geo::RED; };
   if constexpr (!OWN_RED) __syncthreads();
   {
     float *red = red_of(w);
 #pragma unroll
     for (int nb = 0; nb < NB; nb++)
 #pragma unroll
-      for (int v = 0; v < 16; v++) red[(nb * 16 + v) * 64 + lane] = acc[nb][v];
+      for (int cb = 0; cb < NCB; cb++)
+#pragma unroll
+        for (int v = 0; v < NV / NCB; v++) red[(nb * NV + cb * (NV / NCB) + v) * 64 + lane] = acc[nb][cb][v];
   }
   auto reduce_wait = [&]() {
     if (S > 1) {
@@ -671,88 +778,158 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   };
+  auto reduced = [&](int nb, int v) {
+    float sum = red_of(wg0)[(nb * NV + v) * 64 + lane];
+#pragma unroll
+    for (int i = 1; i < 4; i++)
+      if (i < S) sum += red_of(wg0 + i)[(nb * NV + v) * 64 + lane];
+    return sum;
+  };
 
-  // Fast path: a full 32-row block whose rows are consecutive output channels (conv, or a convT
-  // block inside one phase, C4 a multiple of 32).  Every lane-dependent part of an output index
-  // (its column, whether that column exists) is computed once; row offsets are wave-uniform.
+  // Fast path: a full block whose rows are consecutive output channels (conv, or a convT block
+  // inside one phase, C4 a multiple of RB).  Every lane-dependent part of an output index (its
+  // column, whether that column exists) is computed once; row offsets are wave-uniform.
   // The residual operands are all loaded before the reduction barrier, so their latency overlaps
   // it (the compiler may not move a load past a store that could alias it; only the lane that
   // writes an element reads its operand, so this is correct when the output overwrites it).
-  const bool fast = (!phase_rows || C4 % 32 == 0) && mb * 32 + 32 <= M && ldy < (1LL << 25) &&
+  const bool fast = (!phase_rows || C4 % RB == 0) && mb * RB + RB <= M && ldy < (1LL << 25) &&
                     ldt < (1LL << 25);
   if (fast) {
-    const int r_tile = phase_rows ? (mb * 32) / C4 : 0;
-    const long long row0 = (long long) mb * 32 - (long long) r_tile * C4;   // first channel
+    const int r_tile = phase_rows ? (mb * RB) / C4 : 0;
+    const long long row0 = (long long) mb * RB - (long long) r_tile * C4;   // first channel
     float *yk = yb + row0 * ldy;
     float *y2k = y2b != nullptr ? y2b + row0 * ldy : nullptr;
     const float *tk = addt >= 0 ? d.epi[addt].t + (long long) b * d.epi[addt].bst + row0 * ldt : nullptr;
     const int ldy32 = (int) ldy, ldt32 = (int) ldt;
+    if constexpr (RB == 32) {
 #pragma unroll
-    for (int nb = 0; nb < NB; nb++) {
-      const long long q = q0 + 32 * nb + l32;
-      const long long col = q * ys + r_tile - ypad;
-      const bool ok = q < qend && col >= 0 && col < Lout;
-      const int cl = ok ? (int) col : 0;
-      const int oy = 4 * half * ldy32 + cl, ot = 4 * half * ldt32 + cl;
-      float rv[4][4];
-      if (addt >= 0) {
+      for (int nb = 0; nb < NB; nb++) {
+        const long long q = q0 + 32 * nb + l32;
+        const long long col = q * ys + r_tile - ypad;
+        const bool ok = q < qend && col >= 0 && col < Lout;
+        const int cl = ok ? (int) col : 0;
+        const int oy = 4 * half * ldy32 + cl, ot = 4 * half * ldt32 + cl;
+        float rv[4][4];
+        if (addt >= 0) {
 #pragma unroll
-        for (int g = 0; g < 4; g++)
-          if (g < ngrp) {
+          for (int g = 0; g < 4; g++)
+            if (g < ngrp) {
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-              rv[g][j] = ok ? tk[ot + (8 * ((v0 >> 2) + g) + j) * ldt32] : 0.0f;
-          }
-      }
-      if (nb == 0) reduce_wait();
-      float val[4][4];
-#pragma unroll
-      for (int g = 0; g < 4; g++)
-        if (g < ngrp) {
-#pragma unroll
-          for (int j = 0; j < 4; j++) {
-            const int v = v0 + 4 * g + j;
-            float sum = red_of(wg0)[(nb * 16 + v) * 64 + lane];
-#pragma unroll
-            for (int i = 1; i < 4; i++)
-              if (i < S) sum += red_of(wg0 + i)[(nb * 16 + v) * 64 + lane];
-            val[g][j] = sum + bsh[8 * (v >> 2) + 4 * half + j];
-          }
+              for (int j = 0; j < 4; j++)
+                rv[g][j] = ok ? tk[ot + (8 * ((v0 >> 2) + g) + j) * ldt32] : 0.0f;
+            }
         }
-      for (int e = 0; e < nepi; e++) {
-        const int op = d.epi[e].op;
-        const float a = d.epi[e].a;
+        if (nb == 0) reduce_wait();
+        float val[4][4];
 #pragma unroll
         for (int g = 0; g < 4; g++)
           if (g < ngrp) {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-              float x = val[g][j];
+              const int v = v0 + 4 * g + j;
+              val[g][j] = reduced(nb, v) + bsh[8 * (v >> 2) + 4 * half + j];
+            }
+          }
+        for (int e = 0; e < nepi; e++) {
+          const int op = d.epi[e].op;
+          const float a = d.epi[e].a;
+#pragma unroll
+          for (int g = 0; g < 4; g++)
+            if (g < ngrp) {
+#pragma unroll
+              for (int j = 0; j < 4; j++) {
+                float x = val[g][j];
+                switch (op) {
+                  case PTK_EPI_LEAKY: x = x >= 0.0f ? x : a * x; break;
+                  case PTK_EPI_RELU: x = x > 0.0f ? x : 0.0f; break;
+                  case PTK_EPI_MULS: x = x * a; break;
+                  case PTK_EPI_ADDS: x = x + a; break;
+                  case PTK_EPI_ADDT: x = e == addt ? x + rv[g][j]
+                                                   : x + d.epi[e].t[(long long) b * d.epi[e].bst +
+                                                                    (row0 + 8 * ((v0 >> 2) + g) + 4 * half + j) * d.epi[e].ldt + cl];
+                    break;
+                  case PTK_EPI_DIVS: x = x / a; break;
+                  default: break;
+                }
+                val[g][j] = x;
+              }
+            }
+        }
+        if (ok) {
+#pragma unroll
+          for (int g = 0; g < 4; g++)
+            if (g < ngrp) {
+#pragma unroll
+              for (int j = 0; j < 4; j++) {
+                const int o = oy + (8 * ((v0 >> 2) + g) + j) * ldy32;
+                yk[o] = val[g][j];
+                if (y2k != nullptr) y2k[o] = val[g][j] >= 0.0f ? val[g][j] : a2 * val[g][j];
+              }
+            }
+        }
+      }
+    } else {
+      // lane (l16, quad): value v = 4*cb + r is row 4*quad + r, column 16*cb + l16 of the block
+      const int orow = 4 * quad;
+#pragma unroll
+      for (int nb = 0; nb < NB; nb++) {
+        bool ok[2];
+        int cl[2];
+#pragma unroll
+        for (int cb = 0; cb < 2; cb++) {
+          const long long q = q0 + 32 * nb + 16 * cb + l16;
+          const long long col = q * ys + r_tile - ypad;
+          ok[cb] = q < qend && col >= 0 && col < Lout;
+          cl[cb] = ok[cb] ? (int) col : 0;
+        }
+        float rv[8];
+        if (addt >= 0) {
+#pragma unroll
+          for (int i = 0; i < 8; i++)
+            if (i < nv) {
+              const int v = v0 + i, cb = v >> 2;
+              rv[i] = ok[cb] ? tk[(orow + (v & 3)) * ldt32 + cl[cb]] : 0.0f;
+            }
+        }
+        if (nb == 0) reduce_wait();
+        float val[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+          if (i < nv) {
+            const int v = v0 + i;
+            val[i] = reduced(nb, v) + bsh[orow + (v & 3)];
+          }
+        for (int e = 0; e < nepi; e++) {
+          const int op = d.epi[e].op;
+          const float a = d.epi[e].a;
+#pragma unroll
+          for (int i = 0; i < 8; i++)
+            if (i < nv) {
+              const int v = v0 + i, cb = v >> 2;
+              float x = val[i];
               switch (op) {
                 case PTK_EPI_LEAKY: x = x >= 0.0f ? x : a * x; break;
                 case PTK_EPI_RELU: x = x > 0.0f ? x : 0.0f; break;
                 case PTK_EPI_MULS: x = x * a; break;
                 case PTK_EPI_ADDS: x = x + a; break;
-                case PTK_EPI_ADDT: x = e == addt ? x + rv[g][j]
+                case PTK_EPI_ADDT: x = e == addt ? x + rv[i]
                                                  : x + d.epi[e].t[(long long) b * d.epi[e].bst +
-                                                                  (row0 + 8 * ((v0 >> 2) + g) + 4 * half + j) * d.epi[e].ldt + cl];
+                                                                  (row0 + orow + (v & 3)) * d.epi[e].ldt + cl[cb]];
                   break;
                 case PTK_EPI_DIVS: x = x / a; break;
                 default: break;
               }
-              val[g][j] = x;
+              val[i] = x;
             }
-          }
-      }
-      if (ok) {
+        }
 #pragma unroll
-        for (int g = 0; g < 4; g++)
-          if (g < ngrp) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-              const int o = oy + (8 * ((v0 >> 2) + g) + j) * ldy32;
-              yk[o] = val[g][j];
-              if (y2k != nullptr) y2k[o] = val[g][j] >= 0.0f ? val[g][j] : a2 * val[g][j];
+        for (int i = 0; i < 8; i++)
+          if (i < nv) {
+            const int v = v0 + i, cb = v >> 2;
+            if (ok[cb]) {
+              const int o = (orow + (v & 3)) * ldy32 + cl[cb];
+              yk[o] = val[i];
+              if (y2k != nullptr) y2k[o] = val[i] >= 0.0f ? val[i] : a2 * val[i];
             }
           }
       }
@@ -763,8 +940,8 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   // General path (partial row blocks, convT phases that straddle a block): per element
   reduce_wait();
   auto emit = [&](int nb, int v, float sum) {
-    const int m = mb * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-    const long long q = q0 + 32 * nb + l32;
+    const int m = mb * RB + vrow(v);
+    const long long q = q0 + vcol(nb, v);
     if (m >= M || q >= qend) return;
     int co = m, r = 0;
     if (phase_rows) {
@@ -773,7 +950,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
     }
     const long long col = q * ys + r - ypad;
     if (col < 0 || col >= Lout) return;
-    float val = sum + bsh[m - mb * 32];
+    float val = sum + bsh[m - mb * RB];
     for (int e = 0; e < nepi; e++) val = epi_apply(val, d.epi[e], b, co, col);
     const long long yi = (long long) co * ldy + col;
     yb[yi] = val;
@@ -783,9 +960,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   for (int nb = 0; nb < NB; nb++)
     for (int vv = 0; vv < nv; vv++) {
       const int v = v0 + vv;
-      float sum = red_of(wg0)[(nb * 16 + v) * 64 + lane];
-      for (int i = 1; i < S; i++) sum += red_of(wg0 + i)[(nb * 16 + v) * 64 + lane];
-      emit(nb, v, sum);
+      emit(nb, v, reduced(nb, v));
     }
 }
 
@@ -804,18 +979,27 @@ static int env_knob_or(const char *name, int dflt) {
   return e ? atoi(e) : dflt;
 }
 
-// Channel split S in {1, 2, 4} (PTK_CONV_SPLIT overrides).  All waves of a launch usually fit on
-// the chip at once, so a launch lasts as long as its busiest SIMD: with W waves over the 1024
-// SIMDs (256 CUs x 4) that SIMD holds ceil(W / 1024) of them while the mean is W / 1024.  Fewer
-// than ~3 waves per SIMD also leave MFMA latency exposed (a lone wave keeps its SIMD's matrix
-// pipe ~60 % busy), and each split step costs its LDS reduction and a share of the edges.  The
-// model below, fitted to decoder shapes measured on MI355X (batch 1 and 22, C 128 / 256, K 3-11),
-// picks the S with the best predicted MFMA occupancy:
-//   eff(S) = [mean / max waves per SIMD] x [latency hiding at the mean] x [split cost]
-// evaluated on ONE batch item's grid.  S fixes the order in which a block's partial sums are
-// added, so choosing it without the batch size makes a batched item's result bit-identical to
+// Tile shape (RB rows, channel split S in {1, 2, 4}; PTK_CONV_RB and PTK_CONV_SPLIT override).
+// All waves of a launch usually fit on the chip at once, so a launch lasts as long as its busiest
+// SIMD: with W waves over the 1024 SIMDs (256 CUs x 4) that SIMD holds ceil(W / 1024) of them
+// while the mean is W / 1024.  Fewer than ~3 waves per SIMD also leave MFMA latency exposed (a
+// lone wave keeps its SIMD's matrix pipe ~60 % busy), and each split step costs its LDS reduction
+// and a share of the edges.  The model below, fitted to decoder shapes measured on MI355X (batch 1
+// and 22, C 128 / 256, K 3-11), picks the shape with the best predicted MFMA occupancy:
+//   eff = [mean / max waves per SIMD] x [latency hiding at the mean] x [split cost]
+//         x [rows that exist / rows computed] x [16-row tile cost]
+// evaluated on ONE batch item's grid.  The shape fixes the order in which a block's partial sums
+// are added, so choosing it without the batch size makes a batched item's result bit-identical to
 // the same item decoded alone (and it measured faster at batch 8 than a batch-aware choice).
+// 16-row tiles double the waves of a grid (and cut the padding of row counts like 72), at twice
+// the window staging and epilogue work per MFMA.  They need the 16-row weight copy (w16) and are
+// offered to single-problem launches only (PTK_CONV_RB=16 forces them on any launch with the
+// copy): the grouped MRF launches at small T ran as fast or faster alone on 16-row tiles, but
+// the concurrent serving step, where other streams fill the chip anyway, lost 1.4 % of its
+// throughput to their extra work per MFMA.  kRb16Cost = 0.7 puts conv_pre (T 226) and conv_post
+// on 16-row tiles and keeps ups.0 / ups.1 on 32-row ones, as measured at batch 1.
 static const double kSimds = 1024.0;
+static const double kRb16Cost = 0.70;
 static double split_eff(long long waves, int S) {
   const double m = (double) waves / kSimds;
   // past residency the extra waves run as one more wave on the SIMDs they land on
@@ -826,38 +1010,54 @@ static double split_eff(long long waves, int S) {
   const double cost = S == 1 ? 1.0 : (S == 2 ? 0.97 : 0.90);
   return balance * hide * cost;
 }
-static int choose_split(const ptk_conv_desc *const *ds, int n, int nb) {
-  const int env = env_knob("PTK_CONV_SPLIT");
-  if (env == 1 || env == 2 || env == 4) return env;
-  int best = 4;
+static int choose_tiles(const ptk_conv_desc *const *ds, int n, int nb, int *rb_out) {
+  const int env_s = env_knob("PTK_CONV_SPLIT"), env_rb = env_knob("PTK_CONV_RB");
+  bool rb16_ok = nb == 1 && (n == 1 || env_rb == 16);
+  for (int i = 0; i < n; i++)
+    if (ds[i]->w16 == nullptr) rb16_ok = false;
+  int best = 4, best_rb = 32;
   double best_eff = -1.0;
-  for (int S = 1; S <= 4; S *= 2) {
-    const int G = 4 / S;
-    long long waves = 0;
-    for (int i = 0; i < n; i++) {
-      const ptk_conv_desc *d = ds[i];
-      waves += 4LL * ((d->M + 31) / 32) * ((d->nq + 32LL * nb * G - 1) / (32LL * nb * G));
-    }
-    const double e = split_eff(waves, S);
-    if (e > best_eff + 1e-9) {
-      best_eff = e;
-      best = S;
+  for (int RB = 32; RB >= 16; RB /= 2) {
+    if (RB == 16 && !rb16_ok) continue;
+    if ((env_rb == 16 || env_rb == 32) && RB != env_rb && (env_rb == 32 || rb16_ok)) continue;
+    for (int S = 1; S <= 4; S *= 2) {
+      if ((env_s == 1 || env_s == 2 || env_s == 4) && S != env_s) continue;
+      const int G = 4 / S;
+      long long waves = 0;
+      double rows = 0.0, rows_run = 0.0;
+      for (int i = 0; i < n; i++) {
+        const ptk_conv_desc *d = ds[i];
+        const long long mt = (d->M + RB - 1) / RB;
+        const long long tiles = mt * ((d->nq + 32LL * nb * G - 1) / (32LL * nb * G));
+        waves += 4LL * tiles;
+        const double work = (double) d->nq * d->K * d->cinp;
+        rows += work * d->M;
+        rows_run += work * (double) (mt * RB);
+      }
+      const double e = split_eff(waves, S) * (rows_run > 0.0 ? rows / rows_run : 1.0) *
+                       (RB == 16 ? kRb16Cost : 1.0);
+      if (e > best_eff + 1e-9) {
+        best_eff = e;
+        best = S;
+        best_rb = RB;
+      }
     }
   }
+  *rb_out = best_rb;
   return best;
 }
 
 // Band height of the XCD-aware tile order: each XCD runs about n / 8 consecutive tiles of the
 // band sequence, R row blocks x (n / 8) / R column tiles, and its L2 fetches R row blocks of
-// weights (32 rows x cin x K) plus (n / 8) / R input column windows (cin x the window width).
+// weights (rb rows x cin x K) plus (n / 8) / R input column windows (cin x the window width).
 // R is the power of two (up to the row blocks of a batch item) that minimises that sum.  When an
 // XCD's run covers a whole batch item or more, R = all rows (bands do not matter then).
-static int xcd_band(const ptk_conv_desc *d, int mt, int nt, int cols_per_tile) {
+static int xcd_band(const ptk_conv_desc *d, int rb, int mt, int nt, int cols_per_tile) {
   const long long tiles = (long long) mt * nt;
   const long long q = (tiles * d->batch + 7) / 8;
   if (q >= tiles) return mt;
   const int kd = (d->K - 1) * d->dil;
-  const double wrow = 32.0 * d->cinp * d->K;
+  const double wrow = (double) rb * d->cinp * d->K;
   const double xcol = (double) d->cin * ((double) cols_per_tile * d->stride + (kd < 0 ? -kd : kd));
   int best = 1;
   double best_cost = -1.0;
@@ -889,25 +1089,25 @@ extern "C" int ptk_conv_mfma_ok(const ptk_conv_desc *d) {
   return 1;
 }
 
-template <int KT, int NB, int IN>
-static void launch_conv(const ConvGroup &g, int nblk, size_t lds, hipStream_t s) {
-  hipLaunchKernelGGL((conv_mfma_kernel<KT, NB, IN>), dim3((unsigned) nblk), dim3(256), lds, s, g);
+template <int KT, int NB, int IN, int RB>
+static void launch_conv(const ConvGroup &g, int nblk, hipStream_t s) {
+  constexpr size_t lds = LdsGeo<NB, RB>::BYTES;
+  hipLaunchKernelGGL((conv_mfma_kernel<KT, NB, IN, RB>), dim3((unsigned) nblk), dim3(256), lds, s, g);
 }
 
-template <int NB, int IN>
-static void launch_conv_k(int kmax, const ConvGroup &g, int nblk, size_t lds, hipStream_t s) {
-  if (kmax <= 3) launch_conv<3, NB, IN>(g, nblk, lds, s);
-  else if (kmax == 4) launch_conv<4, NB, IN>(g, nblk, lds, s);
-  else if (kmax <= 7) launch_conv<7, NB, IN>(g, nblk, lds, s);
-  else if (kmax <= 11) launch_conv<11, NB, IN>(g, nblk, lds, s);
-  else launch_conv<0, NB, IN>(g, nblk, lds, s);
+template <int NB, int IN, int RB>
+static void launch_conv_k(int kmax, const ConvGroup &g, int nblk, hipStream_t s) {
+  if (kmax <= 3) launch_conv<3, NB, IN, RB>(g, nblk, s);
+  else if (kmax == 4) launch_conv<4, NB, IN, RB>(g, nblk, s);
+  else if (kmax <= 7) launch_conv<7, NB, IN, RB>(g, nblk, s);
+  else if (kmax <= 11) launch_conv<11, NB, IN, RB>(g, nblk, s);
+  else launch_conv<0, NB, IN, RB>(g, nblk, s);
 }
 
-template <int NB>
-static void launch_conv_in(int in_op, int kmax, const ConvGroup &g, int nblk, size_t lds,
-                           hipStream_t s) {
-  if (in_op == PTK_IN_LEAKY) launch_conv_k<NB, PTK_IN_LEAKY>(kmax, g, nblk, lds, s);
-  else launch_conv_k<NB, PTK_IN_PLAIN>(kmax, g, nblk, lds, s);
+template <int NB, int RB>
+static void launch_conv_in(int in_op, int kmax, const ConvGroup &g, int nblk, hipStream_t s) {
+  if (in_op == PTK_IN_LEAKY) launch_conv_k<NB, PTK_IN_LEAKY, RB>(kmax, g, nblk, s);
+  else launch_conv_k<NB, PTK_IN_PLAIN, RB>(kmax, g, nblk, s);
 }
 
 extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream) {
@@ -961,7 +1161,8 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
     g.ngroup++;
   }
   if (g.ngroup == 0) return 0;
-  const int S = choose_split(live, g.ngroup, nb), G = 4 / S;
+  int rb = 32;
+  const int S = choose_tiles(live, g.ngroup, nb, &rb), G = 4 / S;
   g.split = S;
   // XCD-aware tile order: opt-in (PTK_XCD_MAP=1).  On the dominant MRF launch it cuts the L2
   // fills by 15 % (FETCH_SIZE 28.7 -> 24.4 MB) but did not make any decoder shape faster: those
@@ -969,20 +1170,18 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
   const int xcd_map = env_knob_or("PTK_XCD_MAP", 0);
   for (int i = 0; i < g.ngroup; i++) {
     const ptk_conv_desc *d = live[i];
-    g.mt[i] = (d->M + 31) / 32;
+    g.mt[i] = (d->M + rb - 1) / rb;
     g.nt[i] = (int) ((d->nq + 32LL * nb * G - 1) / (32LL * nb * G));
-    g.rg[i] = xcd_map ? xcd_band(d, g.mt[i], g.nt[i], 32 * nb * G) : 0;
+    g.rg[i] = xcd_map ? xcd_band(d, rb, g.mt[i], g.nt[i], 32 * nb * G) : 0;
     g.start[i] = total;
     total += g.mt[i] * g.nt[i] * d->batch;
   }
   for (int i = g.ngroup; i <= PTK_MAX_GROUP; i++) g.start[i] = total;
   if (total == 0) return 0;
-  const size_t stage = (size_t) CONV_WAVES * CONV_CK * win_max(nb) * sizeof(float);
-  const size_t redb = (size_t) CONV_WAVES * 16 * nb * 64 * sizeof(float);
-  const size_t lds = (stage > redb ? stage : redb) + 32 * sizeof(float);   // + the block's bias
   hipStream_t s = (hipStream_t) stream;
-  if (nb == 2) launch_conv_in<2>(in_op, kmax, g, total, lds, s);
-  else launch_conv_in<1>(in_op, kmax, g, total, lds, s);
+  if (nb == 2) launch_conv_in<2, 32>(in_op, kmax, g, total, s);
+  else if (rb == 16) launch_conv_in<1, 16>(in_op, kmax, g, total, s);
+  else launch_conv_in<1, 32>(in_op, kmax, g, total, s);
   HCHK(hipGetLastError());
   return 0;
 }
@@ -1387,6 +1586,21 @@ __global__ void mfma_probe_kernel(const float *a, const float *b, float *d) {
 }
 extern "C" int ptk_mfma_probe(const float *a, const float *b, float *d, void *s) {
   hipLaunchKernelGGL(mfma_probe_kernel, dim3(1), dim3(64), 0, (hipStream_t) s, a, b, d);
+  HCHK(hipGetLastError());
+  return 0;
+}
+
+// 16x16x4: lane l holds A[l % 16][l / 16] and B[l / 16][l % 16]; value r of its result is
+// D[4*(l / 16) + r][l % 16], the layout the 16-row conv tiles assume
+__global__ void mfma16_probe_kernel(const float *a, const float *b, float *d) {
+  const int lane = threadIdx.x;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[(lane & 15) * 4 + (lane >> 4)],
+                                             b[(lane >> 4) * 16 + (lane & 15)], acc, 0, 0, 0);
+  for (int r = 0; r < 4; r++) d[(4 * (lane >> 4) + r) * 16 + (lane & 15)] = acc[r];
+}
+extern "C" int ptk_mfma16_probe(const float *a, const float *b, float *d, void *s) {
+  hipLaunchKernelGGL(mfma16_probe_kernel, dim3(1), dim3(64), 0, (hipStream_t) s, a, b, d);
   HCHK(hipGetLastError());
   return 0;
 }

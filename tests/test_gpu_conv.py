@@ -95,6 +95,18 @@ def test_mfma_lane_layout(ctx):
     assert np.allclose(d, a.astype(np.float64) @ b, atol=1e-5), d[:4, :4]
 
 
+def test_mfma16_lane_layout(ctx):
+    """The same for the fp32 16x16x4 builtin: lane l holds A[l % 16][l / 16], B[l / 16][l % 16] and
+    result rows 4*(l / 16) + r of column l % 16 (the layout of the 16-row conv tiles)."""
+    say("mfma16 probe")
+    rng = np.random.default_rng(1)
+    a = rng.standard_normal((16, 4)).astype(np.float32)
+    b = rng.standard_normal((4, 16)).astype(np.float32)
+    d = np.zeros((16, 16), np.float32)
+    assert ctx.lib.ptd_mfma16_probe(ctx.ptr, pkg.fptr(a), pkg.fptr(b), pkg.fptr(d)) == 0
+    assert np.allclose(d, a.astype(np.float64) @ b, atol=1e-5), d[:4, :4]
+
+
 def _gold_conv_cases():
     return sorted({k.split("_")[0] for k in GOLD.files if k.startswith("conv") and not k.startswith("convT")})
 

@@ -224,6 +224,50 @@ def test_xcd_tile_order_same_result(env, T, batch, monkeypatch):
     dz.free(); dw.free()
 
 
+@pytest.mark.parametrize("rb,split", [(16, 1), (16, 2), (16, 4), (32, 1), (32, 2), (32, 4)])
+def test_tile_shapes_vs_oracle(env, rb, split, monkeypatch):
+    """Every tile shape the launcher can pick (16- or 32-row tiles, channel split 1 / 2 / 4; forced
+    through PTK_CONV_RB / PTK_CONV_SPLIT) against the oracle: a conv with a LeakyReLU epilogue,
+    both convT phase forms (input LeakyReLU, C4 = 256 and 128), the 72-row conv_post whose last
+    row block is partial, an MRF stack (grouped K 3 / 7 / 11, residual adds, branch sums) and a
+    whole decode."""
+    ctx, model, ws, bs = env
+    say(f"tile shape rb={rb} split={split}")
+    monkeypatch.setenv("PTK_CONV_RB", str(rb))
+    monkeypatch.setenv("PTK_CONV_SPLIT", str(split))
+    rng = np.random.default_rng(40 + rb + split)
+    cases = [(0, 226, 0.0, 0.1), (1, 61, 0.1, 0.0), (20, 97, 0.1, 0.0), (39, 203, 0.0, 0.0)]
+    for layer, T, in_a, epi_a in cases:
+        g = synth.dec_layer(layer)
+        x = rng.standard_normal((g["cin"], T)).astype(np.float32)
+        xin = np.where(x >= 0, x, np.float32(in_a) * x) if in_a > 0 else x
+        if g.get("convT"):
+            ref = ol.convT(xin, ws[layer], bs[layer], g["cout"], g["K"], g["s"], g["pad"])[0]
+        else:
+            e0 = 1 if epi_a > 0 else 0
+            ref = ol.conv(xin, ws[layer], bs[layer], g["cout"], g["K"], 1, g["pad"], g["d"], e0, 0, epi_a)[0]
+        c4 = (g["cout"] + 3) // 4 * 4
+        dx, dy = dev_of(ctx, x), pkg.DevBuf(c4 * ref.shape[-1])
+        assert ctx.lib.ptd_layer(ctx.ptr, model.ptr, layer, dx.ptr, T, 1, dy.ptr, in_a, epi_a) == 0
+        y = dy.download(ctx).reshape(c4, -1)
+        e = relerr(y, ref)
+        say(f"  layer {layer} T={T}: {e:.3g}")
+        assert e < TOL, layer
+        dx.free(); dy.free()
+    x = rng.standard_normal((128, 300)).astype(np.float32)
+    ref = ol.mrf(ws[21:39], bs[21:39], x, 0.1)
+    dx, dy = dev_of(ctx, x), pkg.DevBuf(128 * 300)
+    assert ctx.lib.ptd_mrf(ctx.ptr, model.ptr, 1, dx.ptr, 300, 0.1, dy.ptr) == 0
+    assert relerr(dy.download(ctx).reshape(128, 300), ref) < TOL
+    dx.free(); dy.free()
+    z = synth.latent(29, 929)
+    ref, rst = ol.decoder(ws, bs, z, stages=True)
+    wav, st = _decode(ctx, model, z, stages=True)
+    for i in range(6):
+        assert relerr(st[i], rst[i]) < TOL, f"stage {i}"
+    assert np_ref.sndr(wav, ref) >= 60.0
+
+
 def _oracle_windows(ws, bs, z, win, ctx_):
     """The reference's overlap-save schedule (main_v21_serve.c:229-257) composed on the oracle."""
     T = z.shape[-1]
