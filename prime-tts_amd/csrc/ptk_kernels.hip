@@ -403,14 +403,45 @@ __device__ __forceinline__ float in_xform(float v, float a) {
 }
 
 // ------------------------------------------------------------------------------ MFMA conv kernel
+// n / d for 0 <= n < 2^24 as (n * m) >> s, m = ceil(2^s / d), s = 24 + ceil(log2 d): the error
+// term n * (m*d - 2^s) / (d * 2^s) stays below 1/d, so the floor is exact.  With n, m and s
+// wave-uniform the division is two scalar multiplies and a shift.
+struct FastDiv {
+  unsigned m;
+  int s;
+};
+static FastDiv fast_div(unsigned d) {
+  int l = 0;
+  while ((1u << l) < d) l++;
+  const int s = 24 + l;
+  return FastDiv{(unsigned) (((1ull << s) + d - 1) / d), s};
+}
+__device__ __forceinline__ int fdiv(int n, FastDiv f) {
+  return (int) (((unsigned long long) (unsigned) n * f.m) >> f.s);
+}
+
+// Per-problem launch facts computed on the host, 64 bytes: one scalar load at kernel entry.
+struct ConvProb {
+  int count;                      // workgroups of the problem (grid row blockIdx.y = problem)
+  int mt;                         // RB-row blocks
+  int nt;                         // column tiles
+  int rg;                         // row blocks per tile band of the XCD-aware order (0: plain order)
+  FastDiv div_tiles;              // by mt * nt (tiles of one batch item)
+  FastDiv div_mt;                 // by mt
+  FastDiv div_phase;              // by C4 / RB (row blocks per convT phase) when one_phase
+  int one_phase;                  // every row block lies inside one phase (conv, or C4 % RB == 0)
+  int fast;                       // output / residual index ranges fit the 32-bit epilogue
+  int addt;                       // the chain's first tensor add, or -1
+  int pad[3];
+};
+static_assert(sizeof(ConvProb) == 64, "one 64-byte scalar load");
+
 struct ConvGroup {
+  ConvProb info[PTK_MAX_GROUP];
   ptk_conv_desc d[PTK_MAX_GROUP];
-  int start[PTK_MAX_GROUP + 1];   // first workgroup of each problem
-  int mt[PTK_MAX_GROUP];          // 32-row blocks per problem
-  int nt[PTK_MAX_GROUP];          // column tiles per problem
-  int rg[PTK_MAX_GROUP];          // row blocks per tile band of the XCD-aware order (0: plain order)
   int ngroup;
   int split;                      // waves of a workgroup sharing one output block: 1, 2 or 4
+  int lg_split;                   // log2(split)
 };
 
 // Staged input window of one chunk (8 channels): NB column blocks of 32 outputs need
@@ -429,8 +460,8 @@ template <int NB> struct WinGeo {
 // column block; planes are XWMAX + 16 float2 apart, so the two quarter-waves served together
 // fall on different banks.
 //
-// LDS of one workgroup: per wave its staging area, the partial-sum area (the staging area itself
-// when the partial sums fit in it), then the block's RB bias values.
+// LDS of one workgroup: per wave its staging area, and the partial-sum area (the staging area
+// itself when the partial sums fit in it).
 template <int NB, int RB> struct LdsGeo {
   static constexpr int XWMAX = WinGeo<NB>::XWMAX;
   static constexpr int PS = RB == 32 ? XWMAX : XWMAX + 16;   // plane stride (float4 / float2)
@@ -438,8 +469,7 @@ template <int NB, int RB> struct LdsGeo {
   static constexpr int NV = RB / 2;                          // accumulators per lane and column block
   static constexpr int RED = NB * NV * 64;                   // partial-sum floats per wave
   static constexpr bool OWN_RED = RED <= STG;
-  static constexpr int BIAS = CONV_WAVES * (STG > RED ? STG : RED);
-  static constexpr size_t BYTES = (size_t) (BIAS + RB) * sizeof(float);
+  static constexpr size_t BYTES = (size_t) CONV_WAVES * (STG > RED ? STG : RED) * sizeof(float);
 };
 
 // word 3 of a raw buffer resource on gfx9-family parts (gfx950): 32-bit data, range checked
@@ -474,14 +504,14 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   constexpr int NJ = WinGeo<NB>::NJ, XWMAX = WinGeo<NB>::XWMAX;
   using Geo = LdsGeo<NB, RB>;
   constexpr int PS = Geo::PS, NV = Geo::NV;
+  // Grid row blockIdx.y is the problem, so every field of it can be fetched at entry; rows are
+  // as long as the largest problem's workgroup count, and the excess of a shorter one exits.
+  const int p = blockIdx.y;
+  const ConvProb pi = g.info[p];
   int bid = blockIdx.x;
-  int p = 0;
-#pragma unroll
-  for (int i = 1; i < PTK_MAX_GROUP; i++)
-    if (i < g.ngroup && bid >= g.start[i]) p = i;
+  if (bid >= pi.count) return;
   const ptk_conv_desc &d = g.d[p];
-  bid -= g.start[p];
-  const int mt = g.mt[p], nt = g.nt[p], rgh = g.rg[p];
+  const int mt = pi.mt, nt = pi.nt, rgh = pi.rg;
   int b, mb, tn;
   if (rgh > 0) {
     // XCD-aware order.  Workgroups are handed to the 8 XCDs in turn, so the workgroups of this
@@ -489,7 +519,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
     // of the tile sequence, and that sequence walks bands of rgh row blocks column by column, so
     // an XCD's L2 holds a few row blocks of weights and the input columns of its tile run instead
     // of one row block and every input column.  A bijection on [0, n): the result is unchanged.
-    const int n = g.start[p + 1] - g.start[p];
+    const int n = pi.count;
     const int base = n >> 3, rem = n & 7, rho = bid & 7;
     const int tau = rho * base + (rho < rem ? rho : rem) + (bid >> 3);
     b = tau / (mt * nt);
@@ -500,12 +530,12 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
     tn = r / h;
     mb = band * rgh + (r - tn * h);
   } else {
-    b = bid / (mt * nt);
-    bid -= b * mt * nt;
-    mb = bid % mt;
-    tn = bid / mt;
+    b = fdiv(bid, pi.div_tiles);
+    const int r = bid - b * (mt * nt);
+    tn = fdiv(r, pi.div_mt);
+    mb = r - tn * mt;
   }
-  const int S = g.split, G = 4 / S;
+  const int S = g.split, lgS = g.lg_split, G = 4 >> lgS;
 
   // descriptor fields used in loops, read once (the problem index is dynamic, so the compiler
   // would otherwise re-read them from the kernel arguments)
@@ -514,23 +544,34 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   const long long lim = d.lim;
   const float in_a = d.in_a;
   const int nchunk = d.cinp / CONV_CK;          // chunks over all channels
-  const int nch = nchunk / S;                   // chunks of this wave
+  const int nch = nchunk >> lgS;                // chunks of this wave
 
   const int lane = threadIdx.x & 63;
   // wave index: uniform across the wave, which the compiler cannot see on its own (without this
   // the wave-based buffer resources would be treated as divergent)
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int ks = w % S, cg = w / S;             // channel split index, column group
-  // The block's RB bias values go to LDS once, past the staging / reduction area, so that the
-  // epilogue adds them from LDS: a global load per element there, placed after the previous
-  // element's stores, would wait out a whole memory latency each time.
-  float *bsh = smem + Geo::BIAS;
-  if (w == 0 && lane < RB) {
-    const int m = mb * RB + lane;
-    int co = m;
-    if (d.C4 != d.M) co = m - (m / d.C4) * d.C4;
-    bsh[lane] = (d.bias != nullptr && m < d.M && co < d.nbias) ? d.bias[co] : 0.0f;
-  }
+  const int ks = w & (S - 1), cg = w >> lgS;    // channel split index, column group
+  // The phase of this row block (convT: row m is phase m / C4 of channel m % C4), when the block
+  // lies inside one phase.
+  const bool phase_rows = d.C4 != d.M;
+  const bool one_phase = pi.one_phase != 0;
+  const int r_tile = phase_rows && one_phase ? fdiv(mb, pi.div_phase) : 0;
+  // Lane l < RB loads the bias of the block's row l once the first chunk's loads are in flight,
+  // and the epilogue fetches each value's bias from the lane of its row (ds_bpermute): the load's
+  // latency is spent behind the main loop, and no wave depends on another's write.
+  float bias_r = 0.0f;
+  auto load_bias = [&]() {
+    if (lane < RB) {
+      const int m = mb * RB + lane;
+      int co = m;
+      if (phase_rows) co = one_phase ? m - r_tile * d.C4 : m % d.C4;
+      if (d.bias != nullptr && m < d.M && co < d.nbias) bias_r = d.bias[co];
+    }
+  };
+  // bias of row `row` of the block (every lane of the wave must be active)
+  auto bias_of = [&](int row) {
+    return __int_as_float(__builtin_amdgcn_ds_bpermute(row * 4, __float_as_int(bias_r)));
+  };
   const int half = lane >> 5;     // RB = 32: which of the two reduction rows this lane feeds
   const int l32 = lane & 31;
   const int quad = lane >> 4;     // RB = 16: the reduction index (and row group) of this lane
@@ -711,6 +752,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
 #pragma unroll
       for (int k = 0; k < KC; k++) acur[k] = wa(k, 0);
     }
+    load_bias();
     for (int j = 0; j + 1 < nch; j++) chunk(j, std::true_type{});
     chunk(nch - 1, std::false_type{});
   };
@@ -744,13 +786,8 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   float *yb = d.y + (long long) b * d.bsy;
   float *y2b = d.y2 != nullptr ? d.y2 + (long long) b * d.bsy : nullptr;
   const float a2 = d.a2;
-  const bool phase_rows = C4 != M;   // convT: row m is phase m / C4 of channel m % C4
-  // the tensor-add operand of the chain (the residual), if any
-  int addt = -1;
-  for (int e = 0; e < nepi; e++)
-    if (addt < 0 && d.epi[e].op == PTK_EPI_ADDT) addt = e;
-  const long long ldt = addt >= 0 ? d.epi[addt].ldt : 0;
-  const int nv = NV / S, v0 = ks * nv, ngrp = nv / 4, wg0 = cg * S;
+  const int addt = pi.addt;   // the chain's residual add, if any
+  const int nv = NV >> lgS, v0 = ks * nv, ngrp = nv / 4, wg0 = cg * S;
   // row and column of value v inside the block, lane parts included
   auto vrow = [&](int v) { return RB == 32 ? 8 * (v >> 2) + 4 * half + (v & 3) : 4 * quad + (v & 3); };
   auto vcol = [&](int nb, int v) { return RB == 32 ? 32 * nb + l32 : 32 * nb + 16 * (v >> 2) + l16; };
@@ -785,30 +822,51 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
       if (i < S) sum += red_of(wg0 + i)[(nb * NV + v) * 64 + lane];
     return sum;
   };
+  // one epilogue op on value x (rv: its residual when op e is the chain's residual add; another
+  // tensor add reads its operand at (row, col) of this block's channels)
+  auto chain_op = [&](int e, int op, float a, float x, float rv, long long row, int col) {
+    switch (op) {
+      case PTK_EPI_LEAKY: return x >= 0.0f ? x : a * x;
+      case PTK_EPI_RELU: return x > 0.0f ? x : 0.0f;
+      case PTK_EPI_MULS: return x * a;
+      case PTK_EPI_ADDS: return x + a;
+      case PTK_EPI_ADDT:
+        return e == addt ? x + rv : x + d.epi[e].t[(long long) b * d.epi[e].bst + row * d.epi[e].ldt + col];
+      case PTK_EPI_DIVS: return x / a;
+      default: return x;
+    }
+  };
 
   // Fast path: a full block whose rows are consecutive output channels (conv, or a convT block
-  // inside one phase, C4 a multiple of RB).  Every lane-dependent part of an output index (its
-  // column, whether that column exists) is computed once; row offsets are wave-uniform.
-  // The residual operands are all loaded before the reduction barrier, so their latency overlaps
-  // it (the compiler may not move a load past a store that could alias it; only the lane that
-  // writes an element reads its operand, so this is correct when the output overwrites it).
-  const bool fast = (!phase_rows || C4 % RB == 0) && mb * RB + RB <= M && ldy < (1LL << 25) &&
-                    ldt < (1LL << 25);
-  if (fast) {
-    const int r_tile = phase_rows ? (mb * RB) / C4 : 0;
+  // inside one phase), with every index of the output, its LeakyReLU copy and the residual inside
+  // 32 bits (the launcher checks the extents).  Addresses are a wave-uniform row offset, in the
+  // scalar offset of a buffer access, plus a lane offset computed once per column; the residual
+  // loads are issued before the reduction barrier, at a clamped column so that every lane loads
+  // in bounds without a branch (a lane whose column does not exist stores nothing).
+  if (pi.fast && one_phase && mb * RB + RB <= M) {
     const long long row0 = (long long) mb * RB - (long long) r_tile * C4;   // first channel
-    float *yk = yb + row0 * ldy;
-    float *y2k = y2b != nullptr ? y2b + row0 * ldy : nullptr;
-    const float *tk = addt >= 0 ? d.epi[addt].t + (long long) b * d.epi[addt].bst + row0 * ldt : nullptr;
-    const int ldy32 = (int) ldy, ldt32 = (int) ldt;
+    const int ldy32 = (int) ldy;
+    const int ldt32 = addt >= 0 ? (int) d.epi[addt].ldt : 0;
+    const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
+        (void *) (yb + row0 * ldy), (short) 0, (int) 0x7fffffff, PTK_BUF_WORD3);
+    const __amdgpu_buffer_rsrc_t ry2 = __builtin_amdgcn_make_buffer_rsrc(
+        (void *) (y2b != nullptr ? y2b + row0 * ldy : yb), (short) 0, (int) 0x7fffffff, PTK_BUF_WORD3);
+    const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc(
+        (void *) (addt >= 0 ? d.epi[addt].t + (long long) b * d.epi[addt].bst + row0 * ldt32 : yb),
+        (short) 0, (int) 0x7fffffff, PTK_BUF_WORD3);
+    const int q0i = (int) q0, qendi = (int) qend, louti = (int) Lout;
+    auto store = [&](float x, unsigned voff, unsigned soff) {
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), ry, voff, soff, 0);
+      if (y2b != nullptr) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x >= 0.0f ? x : a2 * x), ry2, voff, soff, 0);
+    };
     if constexpr (RB == 32) {
 #pragma unroll
       for (int nb = 0; nb < NB; nb++) {
-        const long long q = q0 + 32 * nb + l32;
-        const long long col = q * ys + r_tile - ypad;
-        const bool ok = q < qend && col >= 0 && col < Lout;
-        const int cl = ok ? (int) col : 0;
-        const int oy = 4 * half * ldy32 + cl, ot = 4 * half * ldt32 + cl;
+        const int q = q0i + 32 * nb + l32;
+        const int col = q * ys + r_tile - ypad;
+        const bool ok = q < qendi && col >= 0 && col < louti;
+        const int cl = ok ? col : 0;
+        const unsigned vy = (unsigned) (4 * half * ldy32 + cl) * 4u, vt = (unsigned) (4 * half * ldt32 + cl) * 4u;
         float rv[4][4];
         if (addt >= 0) {
 #pragma unroll
@@ -816,19 +874,23 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
             if (g < ngrp) {
 #pragma unroll
               for (int j = 0; j < 4; j++)
-                rv[g][j] = ok ? tk[ot + (8 * ((v0 >> 2) + g) + j) * ldt32] : 0.0f;
+                rv[g][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                    rt, vt, (unsigned) ((8 * ((v0 >> 2) + g) + j) * ldt32) * 4u, 0));
             }
         }
-        if (nb == 0) reduce_wait();
         float val[4][4];
 #pragma unroll
         for (int g = 0; g < 4; g++)
           if (g < ngrp) {
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-              const int v = v0 + 4 * g + j;
-              val[g][j] = reduced(nb, v) + bsh[8 * (v >> 2) + 4 * half + j];
-            }
+            for (int j = 0; j < 4; j++) val[g][j] = bias_of(8 * ((v0 >> 2) + g) + 4 * half + j);
+          }
+        if (nb == 0) reduce_wait();
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+          if (g < ngrp) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) val[g][j] += reduced(nb, v0 + 4 * g + j);
           }
         for (int e = 0; e < nepi; e++) {
           const int op = d.epi[e].op;
@@ -837,22 +899,9 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
           for (int g = 0; g < 4; g++)
             if (g < ngrp) {
 #pragma unroll
-              for (int j = 0; j < 4; j++) {
-                float x = val[g][j];
-                switch (op) {
-                  case PTK_EPI_LEAKY: x = x >= 0.0f ? x : a * x; break;
-                  case PTK_EPI_RELU: x = x > 0.0f ? x : 0.0f; break;
-                  case PTK_EPI_MULS: x = x * a; break;
-                  case PTK_EPI_ADDS: x = x + a; break;
-                  case PTK_EPI_ADDT: x = e == addt ? x + rv[g][j]
-                                                   : x + d.epi[e].t[(long long) b * d.epi[e].bst +
-                                                                    (row0 + 8 * ((v0 >> 2) + g) + 4 * half + j) * d.epi[e].ldt + cl];
-                    break;
-                  case PTK_EPI_DIVS: x = x / a; break;
-                  default: break;
-                }
-                val[g][j] = x;
-              }
+              for (int j = 0; j < 4; j++)
+                val[g][j] = chain_op(e, op, a, val[g][j], rv[g][j],
+                                     row0 + 8 * ((v0 >> 2) + g) + 4 * half + j, cl);
             }
         }
         if (ok) {
@@ -860,11 +909,8 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
           for (int g = 0; g < 4; g++)
             if (g < ngrp) {
 #pragma unroll
-              for (int j = 0; j < 4; j++) {
-                const int o = oy + (8 * ((v0 >> 2) + g) + j) * ldy32;
-                yk[o] = val[g][j];
-                if (y2k != nullptr) y2k[o] = val[g][j] >= 0.0f ? val[g][j] : a2 * val[g][j];
-              }
+              for (int j = 0; j < 4; j++)
+                store(val[g][j], vy, (unsigned) ((8 * ((v0 >> 2) + g) + j) * ldy32) * 4u);
             }
         }
       }
@@ -877,67 +923,52 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
         int cl[2];
 #pragma unroll
         for (int cb = 0; cb < 2; cb++) {
-          const long long q = q0 + 32 * nb + 16 * cb + l16;
-          const long long col = q * ys + r_tile - ypad;
-          ok[cb] = q < qend && col >= 0 && col < Lout;
-          cl[cb] = ok[cb] ? (int) col : 0;
+          const int q = q0i + 32 * nb + 16 * cb + l16;
+          const int col = q * ys + r_tile - ypad;
+          ok[cb] = q < qendi && col >= 0 && col < louti;
+          cl[cb] = ok[cb] ? col : 0;
         }
         float rv[8];
         if (addt >= 0) {
 #pragma unroll
           for (int i = 0; i < 8; i++)
             if (i < nv) {
-              const int v = v0 + i, cb = v >> 2;
-              rv[i] = ok[cb] ? tk[(orow + (v & 3)) * ldt32 + cl[cb]] : 0.0f;
+              const int v = v0 + i;
+              rv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                  rt, (unsigned) (orow * ldt32 + cl[v >> 2]) * 4u, (unsigned) ((v & 3) * ldt32) * 4u, 0));
             }
         }
-        if (nb == 0) reduce_wait();
         float val[8];
 #pragma unroll
         for (int i = 0; i < 8; i++)
-          if (i < nv) {
-            const int v = v0 + i;
-            val[i] = reduced(nb, v) + bsh[orow + (v & 3)];
-          }
+          if (i < nv) val[i] = bias_of(orow + ((v0 + i) & 3));
+        if (nb == 0) reduce_wait();
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+          if (i < nv) val[i] += reduced(nb, v0 + i);
         for (int e = 0; e < nepi; e++) {
           const int op = d.epi[e].op;
           const float a = d.epi[e].a;
 #pragma unroll
           for (int i = 0; i < 8; i++)
             if (i < nv) {
-              const int v = v0 + i, cb = v >> 2;
-              float x = val[i];
-              switch (op) {
-                case PTK_EPI_LEAKY: x = x >= 0.0f ? x : a * x; break;
-                case PTK_EPI_RELU: x = x > 0.0f ? x : 0.0f; break;
-                case PTK_EPI_MULS: x = x * a; break;
-                case PTK_EPI_ADDS: x = x + a; break;
-                case PTK_EPI_ADDT: x = e == addt ? x + rv[i]
-                                                 : x + d.epi[e].t[(long long) b * d.epi[e].bst +
-                                                                  (row0 + orow + (v & 3)) * d.epi[e].ldt + cl[cb]];
-                  break;
-                case PTK_EPI_DIVS: x = x / a; break;
-                default: break;
-              }
-              val[i] = x;
+              const int v = v0 + i;
+              val[i] = chain_op(e, op, a, val[i], rv[i], row0 + orow + (v & 3), cl[v >> 2]);
             }
         }
 #pragma unroll
         for (int i = 0; i < 8; i++)
           if (i < nv) {
             const int v = v0 + i, cb = v >> 2;
-            if (ok[cb]) {
-              const int o = (orow + (v & 3)) * ldy32 + cl[cb];
-              yk[o] = val[i];
-              if (y2k != nullptr) y2k[o] = val[i] >= 0.0f ? val[i] : a2 * val[i];
-            }
+            if (ok[cb]) store(val[i], (unsigned) (orow * ldy32 + cl[cb]) * 4u, (unsigned) ((v & 3) * ldy32) * 4u);
           }
       }
     }
     return;
   }
 
-  // General path (partial row blocks, convT phases that straddle a block): per element
+  // General path (partial row blocks, convT phases that straddle a block, large tensors): per
+  // element
   reduce_wait();
   auto emit = [&](int nb, int v, float sum) {
     const int m = mb * RB + vrow(v);
@@ -950,7 +981,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
     }
     const long long col = q * ys + r - ypad;
     if (col < 0 || col >= Lout) return;
-    float val = sum + bsh[m - mb * RB];
+    float val = sum;
     for (int e = 0; e < nepi; e++) val = epi_apply(val, d.epi[e], b, co, col);
     const long long yi = (long long) co * ldy + col;
     yb[yi] = val;
@@ -960,7 +991,8 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   for (int nb = 0; nb < NB; nb++)
     for (int vv = 0; vv < nv; vv++) {
       const int v = v0 + vv;
-      emit(nb, v, reduced(nb, v));
+      const float bv = bias_of(vrow(v));   // all lanes active here
+      emit(nb, v, reduced(nb, v) + bv);
     }
 }
 
@@ -1090,24 +1122,24 @@ extern "C" int ptk_conv_mfma_ok(const ptk_conv_desc *d) {
 }
 
 template <int KT, int NB, int IN, int RB>
-static void launch_conv(const ConvGroup &g, int nblk, hipStream_t s) {
+static void launch_conv(const ConvGroup &g, dim3 grid, hipStream_t s) {
   constexpr size_t lds = LdsGeo<NB, RB>::BYTES;
-  hipLaunchKernelGGL((conv_mfma_kernel<KT, NB, IN, RB>), dim3((unsigned) nblk), dim3(256), lds, s, g);
+  hipLaunchKernelGGL((conv_mfma_kernel<KT, NB, IN, RB>), grid, dim3(256), lds, s, g);
 }
 
 template <int NB, int IN, int RB>
-static void launch_conv_k(int kmax, const ConvGroup &g, int nblk, hipStream_t s) {
-  if (kmax <= 3) launch_conv<3, NB, IN, RB>(g, nblk, s);
-  else if (kmax == 4) launch_conv<4, NB, IN, RB>(g, nblk, s);
-  else if (kmax <= 7) launch_conv<7, NB, IN, RB>(g, nblk, s);
-  else if (kmax <= 11) launch_conv<11, NB, IN, RB>(g, nblk, s);
-  else launch_conv<0, NB, IN, RB>(g, nblk, s);
+static void launch_conv_k(int kmax, const ConvGroup &g, dim3 grid, hipStream_t s) {
+  if (kmax <= 3) launch_conv<3, NB, IN, RB>(g, grid, s);
+  else if (kmax == 4) launch_conv<4, NB, IN, RB>(g, grid, s);
+  else if (kmax <= 7) launch_conv<7, NB, IN, RB>(g, grid, s);
+  else if (kmax <= 11) launch_conv<11, NB, IN, RB>(g, grid, s);
+  else launch_conv<0, NB, IN, RB>(g, grid, s);
 }
 
 template <int NB, int RB>
-static void launch_conv_in(int in_op, int kmax, const ConvGroup &g, int nblk, hipStream_t s) {
-  if (in_op == PTK_IN_LEAKY) launch_conv_k<NB, PTK_IN_LEAKY, RB>(kmax, g, nblk, s);
-  else launch_conv_k<NB, PTK_IN_PLAIN, RB>(kmax, g, nblk, s);
+static void launch_conv_in(int in_op, int kmax, const ConvGroup &g, dim3 grid, hipStream_t s) {
+  if (in_op == PTK_IN_LEAKY) launch_conv_k<NB, PTK_IN_LEAKY, RB>(kmax, g, grid, s);
+  else launch_conv_k<NB, PTK_IN_PLAIN, RB>(kmax, g, grid, s);
 }
 
 extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream) {
@@ -1161,27 +1193,52 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
     g.ngroup++;
   }
   if (g.ngroup == 0) return 0;
-  int rb = 32;
+  int rb = 32, maxcount = 0;
   const int S = choose_tiles(live, g.ngroup, nb, &rb), G = 4 / S;
   g.split = S;
+  g.lg_split = S == 4 ? 2 : S == 2 ? 1 : 0;
   // XCD-aware tile order: opt-in (PTK_XCD_MAP=1).  On the dominant MRF launch it cuts the L2
   // fills by 15 % (FETCH_SIZE 28.7 -> 24.4 MB) but did not make any decoder shape faster: those
   // fills mostly hit the MALL and the launch is bound by MFMA time and its fixed edges.
   const int xcd_map = env_knob_or("PTK_XCD_MAP", 0);
   for (int i = 0; i < g.ngroup; i++) {
     const ptk_conv_desc *d = live[i];
-    g.mt[i] = (d->M + rb - 1) / rb;
-    g.nt[i] = (int) ((d->nq + 32LL * nb * G - 1) / (32LL * nb * G));
-    g.rg[i] = xcd_map ? xcd_band(d, rb, g.mt[i], g.nt[i], 32 * nb * G) : 0;
-    g.start[i] = total;
-    total += g.mt[i] * g.nt[i] * d->batch;
+    ConvProb &pi = g.info[i];
+    pi.mt = (d->M + rb - 1) / rb;
+    pi.nt = (int) ((d->nq + 32LL * nb * G - 1) / (32LL * nb * G));
+    pi.rg = xcd_map ? xcd_band(d, rb, pi.mt, pi.nt, 32 * nb * G) : 0;
+    const long long n = (long long) pi.mt * pi.nt * d->batch;
+    if (n >= (1LL << 24) || total + n >= (1LL << 31)) {
+      set_err("ptk_conv_launch: %lld workgroups for one problem (the tile decode takes < 2^24)", n);
+      return -1;
+    }
+    total += (int) n;
+    pi.count = (int) n;
+    if (pi.count > maxcount) maxcount = pi.count;
+    pi.div_tiles = fast_div((unsigned) (pi.mt * pi.nt));
+    pi.div_mt = fast_div((unsigned) pi.mt);
+    pi.one_phase = d->C4 == d->M || d->C4 % rb == 0;
+    pi.div_phase = fast_div(d->C4 == d->M ? 1u : (unsigned) (d->C4 / rb > 0 ? d->C4 / rb : 1));
+    pi.addt = -1;
+    for (int e = 0; e < d->nepi; e++)
+      if (pi.addt < 0 && d->epi[e].op == PTK_EPI_ADDT) pi.addt = e;
+    // the fast epilogue's 32-bit indices: columns, and byte offsets from a row block's first row
+    const long long lim31 = 1LL << 31, lim30 = 1LL << 30;
+    bool fast = pi.one_phase && d->ldy < (1LL << 23) && d->Lout < lim30 &&
+                (d->q0 + d->nq) * d->ys + d->C4 < lim30 && d->q0 >= 0 &&
+                ((long long) rb * d->ldy + d->Lout) * 4 < lim31;
+    if (pi.addt >= 0) {
+      const long long ldt = d->epi[pi.addt].ldt;
+      fast = fast && ldt >= 0 && ldt < (1LL << 23) && ((long long) rb * ldt + d->Lout) * 4 < lim31;
+    }
+    pi.fast = fast;
   }
-  for (int i = g.ngroup; i <= PTK_MAX_GROUP; i++) g.start[i] = total;
   if (total == 0) return 0;
   hipStream_t s = (hipStream_t) stream;
-  if (nb == 2) launch_conv_in<2, 32>(in_op, kmax, g, total, s);
-  else if (rb == 16) launch_conv_in<1, 16>(in_op, kmax, g, total, s);
-  else launch_conv_in<1, 32>(in_op, kmax, g, total, s);
+  const dim3 grid((unsigned) maxcount, (unsigned) g.ngroup);
+  if (nb == 2) launch_conv_in<2, 32>(in_op, kmax, g, grid, s);
+  else if (rb == 16) launch_conv_in<1, 16>(in_op, kmax, g, grid, s);
+  else launch_conv_in<1, 32>(in_op, kmax, g, grid, s);
   HCHK(hipGetLastError());
   return 0;
 }
