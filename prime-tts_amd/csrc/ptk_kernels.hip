@@ -432,12 +432,29 @@ struct ConvProb {
   int one_phase;                  // every row block lies inside one phase (conv, or C4 % RB == 0)
   int fast;                       // output / residual index ranges fit the 32-bit epilogue
   int addt;                       // the chain's first tensor add, or -1
-  int pad[3];
+  int M;                          // GEMM rows
+  int pad[2];
 };
 static_assert(sizeof(ConvProb) == 64, "one 64-byte scalar load");
 
+// What the fast epilogue reads, 128 bytes per problem, fetched in one batch of scalar loads when
+// the epilogue starts (field by field from the descriptor, each chain op's fields had been a
+// scalar load and a wait of their own).
+struct ConvEpi {
+  const float *y, *y2, *t;        // output, its LeakyReLU copy (or null), the residual of op addt
+  long long bsy, bst;             // batch strides of y / y2 and of t
+  int ldy, ldt;                   // row strides (fit 32 bits on the fast path)
+  int lout, q0, qend, ys, ypad, C4, nepi;
+  int ops;                        // op e in bits 4e .. 4e + 3
+  float a[PTK_MAX_EPI];
+  float a2;
+  int pad[7];
+};
+static_assert(sizeof(ConvEpi) == 128, "two 64-byte scalar loads");
+
 struct ConvGroup {
   ConvProb info[PTK_MAX_GROUP];
+  ConvEpi ep[PTK_MAX_GROUP];
   ptk_conv_desc d[PTK_MAX_GROUP];
   int ngroup;
   int split;                      // waves of a workgroup sharing one output block: 1, 2 or 4
@@ -576,7 +593,8 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   const int l32 = lane & 31;
   const int quad = lane >> 4;     // RB = 16: the reduction index (and row group) of this lane
   const int l16 = lane & 15;
-  const long long q0 = d.q0 + ((long long) tn * G + cg) * (32 * NB);
+  const int q0off = (tn * G + cg) * (32 * NB);   // this wave's first column past d.q0
+  const long long q0 = d.q0 + q0off;
   const int kd = (K - 1) * dil;
   const int dmin = kd < 0 ? kd : 0;
   const int XW = (32 * NB - 1) * st + (kd < 0 ? -kd : kd) + 1;
@@ -787,7 +805,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   float *y2b = d.y2 != nullptr ? d.y2 + (long long) b * d.bsy : nullptr;
   const float a2 = d.a2;
   const int addt = pi.addt;   // the chain's residual add, if any
-  const int nv = NV >> lgS, v0 = ks * nv, ngrp = nv / 4, wg0 = cg * S;
+  const int nv = NV >> lgS, v0 = ks * nv, wg0 = cg * S;
   // row and column of value v inside the block, lane parts included
   auto vrow = [&](int v) { return RB == 32 ? 8 * (v >> 2) + 4 * half + (v & 3) : 4 * quad + (v & 3); };
   auto vcol = [&](int nb, int v) { return RB == 32 ? 32 * nb + l32 : 32 * nb + 16 * (v >> 2) + l16; };
@@ -822,147 +840,133 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
       if (i < S) sum += red_of(wg0 + i)[(nb * NV + v) * 64 + lane];
     return sum;
   };
-  // one epilogue op on value x (rv: its residual when op e is the chain's residual add; another
-  // tensor add reads its operand at (row, col) of this block's channels)
-  auto chain_op = [&](int e, int op, float a, float x, float rv, long long row, int col) {
-    switch (op) {
-      case PTK_EPI_LEAKY: return x >= 0.0f ? x : a * x;
-      case PTK_EPI_RELU: return x > 0.0f ? x : 0.0f;
-      case PTK_EPI_MULS: return x * a;
-      case PTK_EPI_ADDS: return x + a;
-      case PTK_EPI_ADDT:
-        return e == addt ? x + rv : x + d.epi[e].t[(long long) b * d.epi[e].bst + row * d.epi[e].ldt + col];
-      case PTK_EPI_DIVS: return x / a;
-      default: return x;
-    }
-  };
-
   // Fast path: a full block whose rows are consecutive output channels (conv, or a convT block
   // inside one phase), with every index of the output, its LeakyReLU copy and the residual inside
   // 32 bits (the launcher checks the extents).  Addresses are a wave-uniform row offset, in the
   // scalar offset of a buffer access, plus a lane offset computed once per column; the residual
   // loads are issued before the reduction barrier, at a clamped column so that every lane loads
-  // in bounds without a branch (a lane whose column does not exist stores nothing).
-  if (pi.fast && one_phase && mb * RB + RB <= M) {
-    const long long row0 = (long long) mb * RB - (long long) r_tile * C4;   // first channel
-    const int ldy32 = (int) ldy;
-    const int ldt32 = addt >= 0 ? (int) d.epi[addt].ldt : 0;
+  // in bounds without a branch (a lane whose column does not exist stores nothing).  The values
+  // of a lane are val[i], i < nv: value v0 + i of the block.  The chain runs op by op over all of
+  // them, one branch per op.
+  if (pi.fast && one_phase && mb * RB + RB <= pi.M) {
+    const ConvEpi ep = g.ep[p];
+    constexpr int NMAX = RB == 32 ? 16 : 8;
+    // values come in groups of GRP that a wave finishes together (nv is a multiple of GRP)
+    constexpr int GRP = RB == 32 ? 4 : 2, NG = NMAX / GRP;
+    const int ngrp = nv / GRP;
+    const long long row0 = (long long) mb * RB - (long long) r_tile * ep.C4;   // first channel
+    const int ldy32 = ep.ldy, ldt32 = ep.ldt;
+    float *yk = const_cast<float *>(ep.y) + (long long) b * ep.bsy + row0 * ldy32;
     const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
-        (void *) (yb + row0 * ldy), (short) 0, (int) 0x7fffffff, PTK_BUF_WORD3);
+        (void *) yk, (short) 0, (int) 0x7fffffff, PTK_BUF_WORD3);
     const __amdgpu_buffer_rsrc_t ry2 = __builtin_amdgcn_make_buffer_rsrc(
-        (void *) (y2b != nullptr ? y2b + row0 * ldy : yb), (short) 0, (int) 0x7fffffff, PTK_BUF_WORD3);
+        (void *) (ep.y2 != nullptr ? ep.y2 + (long long) b * ep.bsy + row0 * ldy32 : yk), (short) 0,
+        (int) 0x7fffffff, PTK_BUF_WORD3);
     const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc(
-        (void *) (addt >= 0 ? d.epi[addt].t + (long long) b * d.epi[addt].bst + row0 * ldt32 : yb),
-        (short) 0, (int) 0x7fffffff, PTK_BUF_WORD3);
-    const int q0i = (int) q0, qendi = (int) qend, louti = (int) Lout;
-    auto store = [&](float x, unsigned voff, unsigned soff) {
-      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), ry, voff, soff, 0);
-      if (y2b != nullptr) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x >= 0.0f ? x : a2 * x), ry2, voff, soff, 0);
-    };
-    if constexpr (RB == 32) {
+        (void *) (addt >= 0 ? ep.t + (long long) b * ep.bst + row0 * ldt32 : yk), (short) 0,
+        (int) 0x7fffffff, PTK_BUF_WORD3);
+    // lane part of the row of value i, and its wave-uniform part
+    const int lrow = RB == 32 ? 4 * half : 4 * quad;
+    auto urow = [&](int i) { return RB == 32 ? 8 * (((v0 + i) >> 2)) + ((v0 + i) & 3) : ((v0 + i) & 3); };
 #pragma unroll
-      for (int nb = 0; nb < NB; nb++) {
-        const int q = q0i + 32 * nb + l32;
-        const int col = q * ys + r_tile - ypad;
-        const bool ok = q < qendi && col >= 0 && col < louti;
-        const int cl = ok ? col : 0;
-        const unsigned vy = (unsigned) (4 * half * ldy32 + cl) * 4u, vt = (unsigned) (4 * half * ldt32 + cl) * 4u;
-        float rv[4][4];
-        if (addt >= 0) {
+    for (int nb = 0; nb < NB; nb++) {
+      // columns of this lane: one per column block (RB = 32), two (RB = 16)
+      bool ok[NCB];
+      int cl[NCB];
 #pragma unroll
-          for (int g = 0; g < 4; g++)
-            if (g < ngrp) {
+      for (int cb = 0; cb < NCB; cb++) {
+        const int q = ep.q0 + q0off + 32 * nb + (RB == 32 ? l32 : 16 * cb + l16);
+        const int col = q * ep.ys + r_tile - ep.ypad;
+        ok[cb] = q < ep.qend && col >= 0 && col < ep.lout;
+        cl[cb] = ok[cb] ? col : 0;
+      }
+      auto cbo = [&](int i) { return RB == 32 ? 0 : ((v0 + i) >> 2); };
+      float rv[NMAX], val[NMAX];
+      if (addt >= 0) {
 #pragma unroll
-              for (int j = 0; j < 4; j++)
-                rv[g][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                    rt, vt, (unsigned) ((8 * ((v0 >> 2) + g) + j) * ldt32) * 4u, 0));
-            }
-        }
-        float val[4][4];
+        for (int gg = 0; gg < NG; gg++)
+          if (gg < ngrp)
 #pragma unroll
-        for (int g = 0; g < 4; g++)
-          if (g < ngrp) {
+            for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++)
+            rv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                rt, (unsigned) (lrow * ldt32 + cl[cbo(i)]) * 4u, (unsigned) (urow(i) * ldt32) * 4u, 0));
+      }
 #pragma unroll
-            for (int j = 0; j < 4; j++) val[g][j] = bias_of(8 * ((v0 >> 2) + g) + 4 * half + j);
+      for (int gg = 0; gg < NG; gg++)
+        if (gg < ngrp)
+#pragma unroll
+          for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++) val[i] = bias_of(lrow + urow(i));
+      if (nb == 0) reduce_wait();
+#pragma unroll
+      for (int gg = 0; gg < NG; gg++)
+        if (gg < ngrp)
+#pragma unroll
+          for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++) val[i] += reduced(nb, v0 + i);
+#pragma unroll 1
+      for (int e = 0; e < ep.nepi; e++) {
+        const int op = (ep.ops >> (4 * e)) & 15;
+        const float a = e == 0 ? ep.a[0] : e == 1 ? ep.a[1] : e == 2 ? ep.a[2] : ep.a[3];
+        if (op == PTK_EPI_LEAKY) {
+#pragma unroll
+          for (int gg = 0; gg < NG; gg++)
+            if (gg < ngrp)
+#pragma unroll
+              for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++) val[i] = val[i] >= 0.0f ? val[i] : a * val[i];
+        } else if (op == PTK_EPI_RELU) {
+#pragma unroll
+          for (int gg = 0; gg < NG; gg++)
+            if (gg < ngrp)
+#pragma unroll
+              for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++) val[i] = val[i] > 0.0f ? val[i] : 0.0f;
+        } else if (op == PTK_EPI_MULS) {
+#pragma unroll
+          for (int gg = 0; gg < NG; gg++)
+            if (gg < ngrp)
+#pragma unroll
+              for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++) val[i] = val[i] * a;
+        } else if (op == PTK_EPI_ADDS) {
+#pragma unroll
+          for (int gg = 0; gg < NG; gg++)
+            if (gg < ngrp)
+#pragma unroll
+              for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++) val[i] = val[i] + a;
+        } else if (op == PTK_EPI_DIVS) {
+#pragma unroll
+          for (int gg = 0; gg < NG; gg++)
+            if (gg < ngrp)
+#pragma unroll
+              for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++) val[i] = val[i] / a;
+        } else if (op == PTK_EPI_ADDT) {
+          if (e == addt) {
+#pragma unroll
+            for (int gg = 0; gg < NG; gg++)
+              if (gg < ngrp)
+#pragma unroll
+                for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++) val[i] = val[i] + rv[i];
+          } else {   // a second tensor add (no decoder layer has one): its operand read directly
+            const ptk_epi &ee = d.epi[e];
+#pragma unroll
+            for (int gg = 0; gg < NG; gg++)
+              if (gg < ngrp)
+#pragma unroll
+                for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++)
+                val[i] = val[i] + ee.t[(long long) b * ee.bst + (row0 + lrow + urow(i)) * ee.ldt + cl[cbo(i)]];
           }
-        if (nb == 0) reduce_wait();
-#pragma unroll
-        for (int g = 0; g < 4; g++)
-          if (g < ngrp) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) val[g][j] += reduced(nb, v0 + 4 * g + j);
-          }
-        for (int e = 0; e < nepi; e++) {
-          const int op = d.epi[e].op;
-          const float a = d.epi[e].a;
-#pragma unroll
-          for (int g = 0; g < 4; g++)
-            if (g < ngrp) {
-#pragma unroll
-              for (int j = 0; j < 4; j++)
-                val[g][j] = chain_op(e, op, a, val[g][j], rv[g][j],
-                                     row0 + 8 * ((v0 >> 2) + g) + 4 * half + j, cl);
-            }
-        }
-        if (ok) {
-#pragma unroll
-          for (int g = 0; g < 4; g++)
-            if (g < ngrp) {
-#pragma unroll
-              for (int j = 0; j < 4; j++)
-                store(val[g][j], vy, (unsigned) ((8 * ((v0 >> 2) + g) + j) * ldy32) * 4u);
-            }
         }
       }
-    } else {
-      // lane (l16, quad): value v = 4*cb + r is row 4*quad + r, column 16*cb + l16 of the block
-      const int orow = 4 * quad;
+      // a group shares its column block, so one test covers its stores
 #pragma unroll
-      for (int nb = 0; nb < NB; nb++) {
-        bool ok[2];
-        int cl[2];
+      for (int gg = 0; gg < NG; gg++)
+        if (gg < ngrp && ok[cbo(gg * GRP)]) {
+          const unsigned vo = (unsigned) (lrow * ldy32 + cl[cbo(gg * GRP)]) * 4u;
 #pragma unroll
-        for (int cb = 0; cb < 2; cb++) {
-          const int q = q0i + 32 * nb + 16 * cb + l16;
-          const int col = q * ys + r_tile - ypad;
-          ok[cb] = q < qendi && col >= 0 && col < louti;
-          cl[cb] = ok[cb] ? col : 0;
-        }
-        float rv[8];
-        if (addt >= 0) {
-#pragma unroll
-          for (int i = 0; i < 8; i++)
-            if (i < nv) {
-              const int v = v0 + i;
-              rv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                  rt, (unsigned) (orow * ldt32 + cl[v >> 2]) * 4u, (unsigned) ((v & 3) * ldt32) * 4u, 0));
-            }
-        }
-        float val[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-          if (i < nv) val[i] = bias_of(orow + ((v0 + i) & 3));
-        if (nb == 0) reduce_wait();
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-          if (i < nv) val[i] += reduced(nb, v0 + i);
-        for (int e = 0; e < nepi; e++) {
-          const int op = d.epi[e].op;
-          const float a = d.epi[e].a;
-#pragma unroll
-          for (int i = 0; i < 8; i++)
-            if (i < nv) {
-              const int v = v0 + i;
-              val[i] = chain_op(e, op, a, val[i], rv[i], row0 + orow + (v & 3), cl[v >> 2]);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-          if (i < nv) {
-            const int v = v0 + i, cb = v >> 2;
-            if (ok[cb]) store(val[i], (unsigned) (orow * ldy32 + cl[cb]) * 4u, (unsigned) ((v & 3) * ldy32) * 4u);
+          for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++) {
+            const unsigned so = (unsigned) (urow(i) * ldy32) * 4u;
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val[i]), ry, vo, so, 0);
+            if (ep.y2 != nullptr)
+              __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val[i] >= 0.0f ? val[i] : ep.a2 * val[i]), ry2, vo, so, 0);
           }
-      }
+        }
     }
     return;
   }
@@ -1222,6 +1226,7 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
     pi.addt = -1;
     for (int e = 0; e < d->nepi; e++)
       if (pi.addt < 0 && d->epi[e].op == PTK_EPI_ADDT) pi.addt = e;
+    pi.M = d->M;
     // the fast epilogue's 32-bit indices: columns, and byte offsets from a row block's first row
     const long long lim31 = 1LL << 31, lim30 = 1LL << 30;
     bool fast = pi.one_phase && d->ldy < (1LL << 23) && d->Lout < lim30 &&
@@ -1232,6 +1237,29 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
       fast = fast && ldt >= 0 && ldt < (1LL << 23) && ((long long) rb * ldt + d->Lout) * 4 < lim31;
     }
     pi.fast = fast;
+    ConvEpi &ep = g.ep[i];
+    ep.y = d->y;
+    ep.y2 = d->y2;
+    ep.bsy = d->bsy;
+    ep.t = pi.addt >= 0 ? d->epi[pi.addt].t : nullptr;
+    ep.bst = pi.addt >= 0 ? d->epi[pi.addt].bst : 0;
+    ep.ldy = (int) d->ldy;
+    ep.ldt = pi.addt >= 0 ? (int) d->epi[pi.addt].ldt : 0;
+    ep.lout = (int) d->Lout;
+    ep.q0 = (int) d->q0;
+    ep.qend = (int) (d->q0 + d->nq);
+    ep.ys = d->ys;
+    ep.ypad = d->ypad;
+    ep.C4 = d->C4;
+    ep.nepi = d->nepi;
+    ep.ops = 0;
+    for (int e = 0; e < PTK_MAX_EPI; e++) {
+      const int op = e < d->nepi ? d->epi[e].op : PTK_EPI_NONE;
+      // codes outside the table are no-ops, as in epi_apply
+      ep.ops |= (op >= PTK_EPI_NONE && op <= PTK_EPI_DIVS ? op : PTK_EPI_NONE) << (4 * e);
+      ep.a[e] = e < d->nepi ? d->epi[e].a : 0.0f;
+    }
+    ep.a2 = d->a2;
   }
   if (total == 0) return 0;
   hipStream_t s = (hipStream_t) stream;
