@@ -1467,28 +1467,32 @@ extern "C" int ptk_leaky(const float *a, float *y, int64_t n, float alpha, void 
 //   frame[b][n][t] = hann[n] * sum_k (re Bc[k][n] + im Bs[k][n]),  re/im = exp(p_k) cos/sin(pi sin(p_9+k))
 //   ola[b][j] = sum_{j-4t in [0,16)} frame[b][j-4t][t];   y[b][i] = ola[b][i+8] / max(wsum[i+8], 1e-9)
 //   wav[o] = sum_b sum_m h[b][m] * 4 * y[b][(o+m-31)/4]   over (o+m-31) = 0 mod 4 in range.
-// One workgroup produces TAIL_OUT consecutive samples; it recomputes the ~TAIL_OUT/16 + 5 frames
-// per band it needs (in LDS), so the whole tail is a single pass over p with no intermediates.
-#define TAIL_OUT 512
-// 512 samples per workgroup measured best: 256 recomputes more frames per output (26 for 16),
-// 1024 leaves most CUs idle at batch 1 (57 blocks for one T = 226 request)
-#define TAIL_THREADS 512
-#define TAIL_NY (TAIL_OUT / 4 + 18)
-#define TAIL_NT (TAIL_NY / 4 + 6)
+// One workgroup of TAIL_THREADS threads produces TAIL_OUT consecutive samples; it recomputes the
+// ~TAIL_OUT/16 + 5 frames per band it needs (in LDS), so the whole tail is a single pass over p
+// with no intermediates.  Every sample is computed by the same operations whatever the block
+// size, so the launcher picks the size from the grid without changing a result.
 #define TAIL_KP 12   // a frame's 9 spectrum values padded to 12: three aligned float4 reads
 
+template <int TAIL_OUT, int TAIL_THREADS>
 __global__ void __launch_bounds__(TAIL_THREADS) tail_kernel(const float *__restrict__ p, long long ldp,
                                                         long long bsp, long long L,
                                                         float *__restrict__ wav, long long bsw,
                                                         const float *__restrict__ cst, ptk_emit em) {
+  constexpr int TAIL_NY = TAIL_OUT / 4 + 18, TAIL_NT = TAIL_NY / 4 + 6;
+  static_assert(TAIL_OUT / 4 <= TAIL_THREADS && TAIL_THREADS % 16 == 0, "phase 2 / 4 thread maps");
   // samples of this item that are kept; a block entirely outside them does no work
   const long long e_lo = blockIdx.y == 0 ? em.lo_first : em.lo;
   const long long e_hi = blockIdx.y + 1 == gridDim.y ? em.hi_last : em.hi;
   if ((long long) blockIdx.x * TAIL_OUT >= e_hi || ((long long) blockIdx.x + 1) * TAIL_OUT <= e_lo) return;
-  __shared__ __align__(16) float s_re[4][TAIL_NT][TAIL_KP];
-  __shared__ __align__(16) float s_im[4][TAIL_NT][TAIL_KP];
+  // the spectra (phases 1-2) and the y rows (phases 3-4) are never live together: y reuses the
+  // spectra's LDS, which keeps three 1024-sample blocks resident per CU
+  constexpr int SPEC = 2 * 4 * TAIL_NT * TAIL_KP;
+  static_assert(4 * TAIL_NY <= SPEC, "y fits over the spectra");
+  __shared__ __align__(16) float s_spec[SPEC];
   __shared__ __align__(16) float s_fr[4][TAIL_NT][16];
-  __shared__ float s_y[4][TAIL_NY];
+  auto s_re = reinterpret_cast<float (*)[TAIL_NT][TAIL_KP]>(s_spec);
+  auto s_im = reinterpret_cast<float (*)[TAIL_NT][TAIL_KP]>(s_spec + 4 * TAIL_NT * TAIL_KP);
+  auto s_y = reinterpret_cast<float (*)[TAIL_NY]>(s_spec);
   __shared__ float s_hann[16];
   const int tid = threadIdx.x;
   const float *hann = cst, *bc = cst + 16, *bs = cst + 160, *hp = cst + 304, *hb = cst + 560;
@@ -1635,6 +1639,14 @@ __global__ void __launch_bounds__(TAIL_THREADS) tail_kernel(const float *__restr
   }
 }
 
+template <int TOUT, int THR>
+static void launch_tail(unsigned blocks, int batch, const float *p, int64_t ldp, int64_t bsp,
+                        int64_t L, float *wav, int64_t bsw, const float *consts, ptk_emit em,
+                        hipStream_t s) {
+  hipLaunchKernelGGL((tail_kernel<TOUT, THR>), dim3(blocks, (unsigned) batch), dim3(THR), 0, s, p,
+                     (long long) ldp, (long long) bsp, (long long) L, wav, (long long) bsw, consts, em);
+}
+
 extern "C" int ptk_tail_batched(const float *p, int64_t ldp, int64_t bsp, int64_t L, float *wav,
                                 int64_t bsw, int batch, const float *consts, const ptk_emit *emit,
                                 void *s) {
@@ -1646,9 +1658,20 @@ extern "C" int ptk_tail_batched(const float *p, int64_t ldp, int64_t bsp, int64_
   const long long nout = 16 * (L - 1);
   const ptk_emit all = {0, 0, nout, nout};
   const ptk_emit em = emit ? *emit : all;
-  const unsigned blocks = (unsigned) ((nout + TAIL_OUT - 1) / TAIL_OUT);
-  hipLaunchKernelGGL(tail_kernel, dim3(blocks, (unsigned) batch), dim3(TAIL_THREADS), 0, (hipStream_t) s, p,
-                     (long long) ldp, (long long) bsp, (long long) L, wav, (long long) bsw, consts, em);
+  // Block size: 1024 samples (on 512 threads) once their grid gives every CU a block, else 512.
+  // Measured on MI355X, T = 226 requests: batch 1 5.6 us with 512 (6.9 with 1024: 57 blocks for
+  // 256 CUs), batch 8 9.3 us with 1024 (10.9 with 512), batch 64 45.6 us = 1.79 TB/s with 1024
+  // (61 us with 512): the larger block recomputes fewer halo frames (74 for 64 instead of 42 for
+  // 32) and runs fewer, longer-lived blocks through its three barriers.  PTK_TAIL_OUT=512 / 1024
+  // forces one.
+  const int knob = env_knob("PTK_TAIL_OUT");
+  const long long blocks1k = (nout + 1023) / 1024;
+  const bool big = knob == 1024 || (knob != 512 && blocks1k * batch >= 256);
+  hipStream_t st = (hipStream_t) s;
+  if (big)
+    launch_tail<1024, 512>((unsigned) blocks1k, batch, p, ldp, bsp, L, wav, bsw, consts, em, st);
+  else
+    launch_tail<512, 512>((unsigned) ((nout + 511) / 512), batch, p, ldp, bsp, L, wav, bsw, consts, em, st);
   HCHK(hipGetLastError());
   return 0;
 }

@@ -170,6 +170,30 @@ def test_tail_alone_vs_oracle(env, L, batch):
     dp.free(); dw.free()
 
 
+@pytest.mark.parametrize("L,batch", [(2, 1), (65, 3), (3617, 2)])
+def test_tail_block_size_gives_the_same_samples(env, L, batch, monkeypatch):
+    """The tail kernel's block size (512 or 1024 samples, chosen from the grid; forced here through
+    PTK_TAIL_OUT) only changes which workgroup makes a sample: the waveform is bit-identical, and
+    within the oracle bar."""
+    ctx, model, ws, bs = env
+    say(f"tail block sizes L={L} batch={batch}")
+    rng = np.random.default_rng(7 * L + batch)
+    p = (0.7 * rng.standard_normal((batch, 72, L))).astype(np.float32)
+    dp = dev_of(ctx, p)
+    dw = pkg.DevBuf(batch * 16 * (L - 1))
+    outs = []
+    for size in ("512", "1024"):
+        monkeypatch.setenv("PTK_TAIL_OUT", size)
+        dw.upload(ctx, np.full(batch * 16 * (L - 1), np.nan, np.float32))
+        assert ctx.lib.ptd_tail(ctx.ptr, model.ptr, dp.ptr, L, batch, dw.ptr) == 0
+        outs.append(dw.download(ctx).reshape(batch, 16 * (L - 1)))
+    monkeypatch.delenv("PTK_TAIL_OUT")
+    assert np.array_equal(outs[0], outs[1])
+    for i in range(batch):
+        assert relerr(outs[1][i], ol.tail(p[i], ws[40], bs[40])) < 1e-4
+    dp.free(); dw.free()
+
+
 def test_decoder_final_conv_is_an_input():
     """The final PQMF synthesis conv (layer 40) comes from the caller's weights: a random filter
     with a bias gives the oracle's waveform, not the model constant's."""
