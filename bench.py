@@ -141,6 +141,56 @@ DECODE_LAUNCHES = (
        ("tail: iSTFT + PQMF", "bytes", 4.0 * (72 * _L + 16 * (_L - 1)))])
 
 
+# flop per GEMM column of the 40 conv launches of a decode, in ptd_window_cols order: conv_pre,
+# ups.0 (phase form: a column is 4 outputs of 4 taps each), MRF-256 (depth, branch K 3/7/11,
+# c1 / c2), ups.1, MRF-128, conv_post
+_COL_FLOP = ([2.0 * 512 * 192 * 7, 2.0 * 4 * 256 * 512 * 4]
+             + [2.0 * 256 * 256 * K for _d in range(3) for K in (3, 7, 11) for _c in range(2)]
+             + [2.0 * 4 * 128 * 256 * 4]
+             + [2.0 * 128 * 128 * K for _d in range(3) for K in (3, 7, 11) for _c in range(2)]
+             + [2.0 * 72 * 128 * 7])
+
+
+def window_conv_gflop(lib, T, win, ctx_):
+    """Conv work of ptd_decode_windows(T, win, ctx_) in GFLOP: (the columns it computes, every
+    column of every window).  The schedule restates pt_decoder.c's win_schedule / win_plan_make:
+    full-width windows run as one batched decode, other widths alone; each launch covers the
+    columns ptd_window_cols names."""
+    ws, a, emitted = [], 0, 0
+    while emitted < T:
+        w = min(win, T - a)
+        last = a + w >= T
+        lo, hi = (0 if a == 0 else ctx_), (w if last else w - ctx_)
+        e0, e1 = max(a + lo, emitted), min(a + hi, T)
+        ws.append((a, w, e0, e1))
+        emitted = max(emitted, e1)
+        if last:
+            break
+        a = max(e1 - ctx_, 1)
+    full = [x for x in ws if x[1] == win]
+    runs = [(x[1], 1, (x[2] - x[0], x[2] - x[0], x[3] - x[0], x[3] - x[0])) for x in ws if x[1] != win]
+    if full:
+        f0, fl = full[0], full[-1]
+        runs.append((win, len(full), (f0[2] - f0[0], ctx_, win - ctx_, fl[3] - fl[0])))
+    done = every = 0.0
+    out = (C.c_int64 * (5 * 40))()
+    for width, batch, (lo_first, lo, hi, hi_last) in runs:
+        if lib.ptd_window_cols(width, batch, lo_first * HOP, lo * HOP, hi * HOP, hi_last * HOP, out) < 0:
+            raise RuntimeError("ptd_window_cols failed")
+        for i in range(40):
+            q0, nq, el, er, shape = out[5 * i:5 * i + 5]
+            cols = batch * nq + el + er
+            done += _COL_FLOP[i] * cols
+            every += _COL_FLOP[i] * batch * shape
+    return done / 1e9, every / 1e9
+
+
+def decode_conv_gflop(T):
+    """Conv work of one full decode of T frames in GFLOP (every GEMM column)."""
+    cols = [T, T + 1] + [4 * T] * 18 + [4 * T + 1] + [16 * T] * 18 + [16 * T + 1]
+    return sum(f * c for f, c in zip(_COL_FLOP, cols)) / 1e9
+
+
 _DECODER_KERNELS = ("conv_mfma_kernel", "avg3_leaky_kernel", "tail_kernel")
 GRBM_XCDS, SIMDS = 8, 1024     # GRBM_GUI_ACTIVE sums the 8 XCDs; 256 CUs x 4 SIMDs
 
@@ -609,6 +659,10 @@ def main():
               "chunked_total_ms": round(timer.time(all_chunks, 5), 4),
               "batched_windows_ms": round(timer.time(batched, 10), 4)}
     stream["audio_s"] = round(T_long * HOP / SR, 4)
+    # each window computes only the columns its kept samples depend on (ptd_window_cols)
+    g_done, g_all = window_conv_gflop(lib, T_long, WIN, CTX)
+    stream["batched_windows_conv_gflop"] = {"computed": round(g_done, 2), "all_columns": round(g_all, 2)}
+    stream["batched_windows_tflops"] = round(g_done / stream["batched_windows_ms"], 2)
     for b in (zl, pcm, wl):
         b.free()
     log(f"streaming: {stream}")
@@ -641,6 +695,8 @@ def main():
     value = audio_step * args.steps / dt
     audio8 = sum(Ts) * HOP / SR
     log(f"config 5: {value:.1f} audio-s/s ({dt / args.steps * 1e3:.2f} ms/step)")
+    # conv work of one step as computed: 8 full decodes + the windowed long-form request
+    step_gflop = sum(decode_conv_gflop(T) for T in Ts) + window_conv_gflop(lib, T_long, 96, 16)[0]
     # the timed step's own outputs (after the timed region): the eight requests are compared with
     # the reference's CPU path in the cpu_baseline leg, the long-form windows with one full
     # (unwindowed) decode of the same latents
@@ -683,6 +739,8 @@ def main():
                         "one shared weight set",
             "request_frames": Ts, "longform_frames": T_long, "audio_s_per_step": round(audio_step, 4),
             "audio_s_8_requests": round(audio8, 4), "parallelism": "1 GPU, 9 streams",
+            "step_conv_gflop": round(step_gflop, 2),
+            "step_conv_tflops": round(step_gflop / (dt / args.steps * 1e3), 2),
             "io": "latents and waveforms device-resident in the timed step (uploaded before it, "
                   "read back after it)",
         },

@@ -110,6 +110,11 @@ int ptd_tail(pt_ctx *c, const ptd_model *m, const float *p, int64_t L, int batch
  * the input as it is read; epi_leaky > 0 applies it to the output.  Asynchronous. */
 int ptd_layer(pt_ctx *c, const ptd_model *m, int layer, const float *x, int64_t T, int batch,
               float *y, float in_leaky, float epi_leaky);
+/* The same over a part of the GEMM columns (no counterpart in the reference): cols = {q0, nq,
+ * ext_l, ext_r, nq_shape} as ptd_window_cols gives them (conv: column = output position; convT:
+ * column q writes outputs q*stride - pad .. + stride - 1).  Outputs outside are not written. */
+int ptd_layer_cols(pt_ctx *c, const ptd_model *m, int layer, const float *x, int64_t T, int batch,
+                   float *y, float in_leaky, float epi_leaky, const int64_t *cols);
 /* One MRF stack (config 3): stage 0 = MRF-256 (layers 2..19), 1 = MRF-128 (21..38);
  * x [C][T] -> out = leaky(((b0 + b1) + b2) / 3, alpha) [C][T].  Asynchronous. */
 int ptd_mrf(pt_ctx *c, const ptd_model *m, int stage, const float *x, int64_t T, float alpha,
@@ -142,6 +147,20 @@ size_t ptd_windows_arena_bytes(int64_t T, int win, int ctx);
 int ptd_decode_windows2(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int win_first,
                         int win, int ctx, float *wav);
 size_t ptd_windows2_arena_bytes(int64_t T, int win_first, int win, int ctx);
+/* The columns a windowed decode computes (no counterpart in the reference, which decodes every
+ * column of a window and drops the samples outside its interior): each conv launch covers only
+ * the columns the kept samples depend on, with the tile shape of the full window, so the kept
+ * samples are bit-identical to a full-window decode.  For a decode of `batch` windows of T frames
+ * in which item 0 keeps samples [lo_first, hi), middle items [lo, hi) and the last item
+ * [lo, hi_last) (one item: [lo_first, hi_last)), out[5*i .. 5*i + 4] receives launch i's GEMM
+ * columns {q0, nq, ext_l, ext_r, nq_shape} (ptk_conv_desc: item 0 starts ext_l earlier, the last
+ * item ends ext_r later), launches in decode order: conv_pre, ups.0, MRF-256 (depth, branch
+ * K 3/7/11, c1 then c2: 18), ups.1, MRF-128 (18), conv_post.  Host only.  Returns 1 (columns left
+ * out), 0 (every column is needed: the decode runs whole) or -1 (bad arguments).
+ * PTD_WINDOW_CONE=0 in the environment makes windowed decodes compute every column. */
+#define PTD_WINDOW_LAUNCHES 40
+int ptd_window_cols(int64_t T, int batch, int64_t lo_first, int64_t lo, int64_t hi,
+                    int64_t hi_last, int64_t *out);
 
 /* A decode of fixed shape and buffers captured once as a HIP graph and replayed (no counterpart in
  * the reference, whose graph interpreter issues every node from the host): for a serving loop that
@@ -229,6 +248,10 @@ void ptd_free(void *p);
  * its env knobs only): after `skip` more device allocations of this library succeed, the next n
  * fail as if the device were out of memory.  Process-wide; n = 0 switches it off. */
 void ptd_debug_fail_allocs(int skip, int n);
+/* Tests of what a decode reads (no counterpart in the reference): every byte of the context's
+ * arena set to `byte` on its stream (0xff makes every float NaN, so a column read before any
+ * launch wrote it poisons what depends on it).  Synchronous.  0 / -1. */
+int ptd_debug_fill_arena(pt_ctx *c, int byte);
 int ptd_h2d(pt_ctx *c, void *dst, const void *src, size_t bytes);   /* synchronous */
 int ptd_d2h(pt_ctx *c, void *dst, const void *src, size_t bytes);   /* synchronous */
 int ptd_sync(pt_ctx *c);                        /* wait for the context's stream */

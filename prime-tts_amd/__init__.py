@@ -67,6 +67,8 @@ _SIGS = {
     "ptd_decode_arena_bytes": (C.c_size_t, [I64, C.c_int]),
     "ptd_decode_stages": (C.c_int, [VP, VP, VP, I64, VP, C.POINTER(VP)]),
     "ptd_layer": (C.c_int, [VP, VP, C.c_int, VP, I64, C.c_int, VP, C.c_float, C.c_float]),
+    "ptd_layer_cols": (C.c_int, [VP, VP, C.c_int, VP, I64, C.c_int, VP, C.c_float, C.c_float, VP]),
+    "ptd_window_cols": (C.c_int, [I64, C.c_int, I64, I64, I64, I64, VP]),
     "ptd_tail": (C.c_int, [VP, VP, VP, I64, C.c_int, VP]),
     "ptd_mrf": (C.c_int, [VP, VP, C.c_int, VP, I64, C.c_float, VP]),
     "ptd_mrf_depth": (C.c_int, [VP, VP, C.c_int, C.c_int, C.POINTER(VP), C.POINTER(VP),
@@ -94,6 +96,7 @@ _SIGS = {
     "ptd_malloc": (VP, [C.c_size_t]),
     "ptd_free": (None, [VP]),
     "ptd_debug_fail_allocs": (None, [C.c_int, C.c_int]),
+    "ptd_debug_fill_arena": (C.c_int, [VP, C.c_int]),
     "ptd_h2d": (C.c_int, [VP, VP, VP, C.c_size_t]),
     "ptd_d2h": (C.c_int, [VP, VP, VP, C.c_size_t]),
     "ptd_sync": (C.c_int, [VP]),

@@ -222,12 +222,210 @@ static void epi_push(ptk_conv_desc *d, int op, float a, const float *t, int64_t 
   d->nepi++;
 }
 
+/* ------------------------------------------------------------------ columns a window needs
+ * An overlap-save window keeps only the samples of its interior, and each kept sample depends on
+ * a bounded run of columns of every layer (its dependency cone).  Columns outside the cones of
+ * the kept samples feed nothing that is stored, so a windowed decode computes each layer over the
+ * union of those cones only.  Every column it computes gets the same arithmetic as in the full
+ * window (the tile shape is chosen for the full width, nq_shape), so the kept samples are
+ * bit-identical to those of the full-window decode.  The cones follow the graph backwards from
+ * the kept samples:
+ *   tail: sample s reads the PQMF input slots u in [s - 31, s + 31], nonzero only at u = 4i, and
+ *         y[i] = ola[i + 8] / wsum[i + 8] overlaps frames t with 4t <= i + 8 < 4t + 16;
+ *   conv (stride 1, "same" padding r = dil*(K-1)/2): column t reads [t - r, t + r];
+ *   conv_post reads its (1, 0) reflection-padded input: column t reads input [t - 4, t + 2];
+ *   MRF depth: x' = x + c2(leaky(c1(leaky(x)))): c2 column t reads c1 output [t - r2, t + r2] and
+ *         x at t; c1 column t reads x [t - r1, t + r1] (per branch; the stage input is shared);
+ *   convT phase form (stride s, pad p): GEMM column q writes outputs q*s - p .. q*s - p + s - 1,
+ *         so output o comes from column floor((o + p) / s), and column q reads input
+ *         [q - ntap + 1, q];
+ *   the branch average and LeakyReLU passes are per column.
+ * Bounds move independently, so one pass over [lo, hi) gives the middle items' columns and one
+ * over [lo_first, hi_last) the first item's left and the last item's right end. */
+typedef struct {
+  int64_t a, b;   /* columns [a, b) */
+} span;
+
+/* the columns of one launch (ptk_conv_desc q0, nq, ext_l, ext_r, nq_shape) */
+typedef struct {
+  int64_t q0, nq, ext_l, ext_r, nq_shape;
+} cols_t;
+
+typedef struct {
+  int on;
+  cols_t pre, up0, up1, post;
+  cols_t mrf[2][3][3][2];   /* [stage][depth][branch][c1, c2] */
+} cone_plan;
+
+static int64_t div_floor(int64_t a, int64_t b) { return a >= 0 ? a / b : -((-a + b - 1) / b); }
+static int64_t div_ceil(int64_t a, int64_t b) { return -div_floor(-a, b); }
+static span span_clip(span x, int64_t lo, int64_t hi) {
+  if (x.a < lo) x.a = lo;
+  if (x.b > hi) x.b = hi;
+  return x;
+}
+static span span_grow(span x, int64_t r, int64_t n) {
+  x.a -= r;
+  x.b += r;
+  return span_clip(x, 0, n);
+}
+static span span_union(span x, span y) {
+  if (y.a < x.a) x.a = y.a;
+  if (y.b > x.b) x.b = y.b;
+  return x;
+}
+
+/* convT (stride s, pad p, ntap taps, tin input columns): GEMM columns that produce outputs
+ * [o.a, o.b), within [qlo, qhi] of the full launch, and the input columns they read */
+static span convT_cols(span o, int s, int p, int64_t qlo, int64_t qhi) {
+  span q = {div_ceil(o.a + p - s + 1, s), div_floor(o.b - 1 + p, s) + 1};
+  return span_clip(q, qlo, qhi + 1);
+}
+static span convT_in(span q, int ntap, int64_t tin) {
+  span x = {q.a - ntap + 1, q.b};
+  return span_clip(x, 0, tin);
+}
+
+static void cols_set(cols_t *c, span mid, span ext, int64_t full, int batch) {
+  if (batch == 1) mid = ext;
+  c->q0 = mid.a;
+  c->nq = mid.b - mid.a;
+  c->ext_l = mid.a - ext.a;
+  c->ext_r = ext.b - mid.b;
+  c->nq_shape = full;
+}
+
+/* MRF stage backwards: y[2] = the columns each branch's output must hold (mid / ext); fills the
+ * stage's launches and returns the stage input's columns */
+static void mrf_cols(cols_t (*cols)[3][2], span ymid, span yext, int64_t T, int batch, span *xmid,
+                     span *xext) {
+  span um = {T, 0}, ue = {T, 0};
+  for (int br = 0; br < 3; br++) {
+    const int r2 = (kMrfK[br] - 1) / 2;
+    span ym = ymid, ye = yext;
+    for (int j = 2; j >= 0; j--) {
+      const int r1 = kMrfD[j] * r2;
+      const span am = span_grow(ym, r2, T), ae = span_grow(ye, r2, T);
+      cols_set(&cols[j][br][1], ym, ye, T, batch);
+      cols_set(&cols[j][br][0], am, ae, T, batch);
+      ym = span_union(span_grow(am, r1, T), ym);
+      ye = span_union(span_grow(ae, r1, T), ye);
+    }
+    um = span_union(um, ym);
+    ue = span_union(ue, ye);
+  }
+  *xmid = um;
+  *xext = ue;
+}
+
+/* 0 with the plan filled, -1 when no column can be left out (or the window keeps nothing) */
+static int cone_plan_make(cone_plan *cp, int64_t T, int batch, const ptk_emit *em) {
+  memset(cp, 0, sizeof *cp);
+  const int64_t T1 = 4 * T, T2 = 16 * T, L = T2 + 1, S = 256 * T;
+  span sm = {em->lo, em->hi}, se = {em->lo_first, em->hi_last};
+  if (batch == 1) sm = se;
+  se = span_union(se, sm);
+  sm = span_clip(sm, 0, S);
+  se = span_clip(se, 0, S);
+  if (sm.b <= sm.a) return -1;
+  if (sm.a == 0 && sm.b == S) return -1;   /* every item keeps every sample: full columns */
+  span pm, pe;   /* conv_post output frames */
+  {
+    const span *in[2] = {&sm, &se};
+    span *out[2] = {&pm, &pe};
+    for (int k = 0; k < 2; k++) {
+      const int64_t ilo = div_ceil(in[k]->a - 31, 4), ihi = div_floor(in[k]->b - 1 + 31, 4);
+      span t = {div_ceil(ilo - 7, 4), div_floor(ihi + 8, 4) + 1};
+      *out[k] = span_clip(t, 0, L);
+    }
+  }
+  cols_set(&cp->post, pm, pe, L, batch);
+  /* conv_post input (the averaged MRF-128 output), through the reflection pad */
+  span ym = {pm.a - 4, pm.b + 2}, ye = {pe.a - 4, pe.b + 2};
+  ym = span_clip(ym, 0, T2);
+  ye = span_clip(ye, 0, T2);
+  span xm, xe;
+  mrf_cols(cp->mrf[1], ym, ye, T2, batch, &xm, &xe);
+  /* ups.1: convT 256 -> 128, K16 s4 p6 (4 taps per phase), columns q in [1, T1 + 1] */
+  span qm = convT_cols(xm, 4, 6, 1, T1 + 1), qe = convT_cols(xe, 4, 6, 1, T1 + 1);
+  cols_set(&cp->up1, qm, qe, T1 + 1, batch);
+  ym = convT_in(qm, 4, T1);
+  ye = convT_in(qe, 4, T1);
+  mrf_cols(cp->mrf[0], ym, ye, T1, batch, &xm, &xe);
+  qm = convT_cols(xm, 4, 6, 1, T + 1);
+  qe = convT_cols(xe, 4, 6, 1, T + 1);
+  cols_set(&cp->up0, qm, qe, T + 1, batch);
+  ym = convT_in(qm, 4, T);
+  ye = convT_in(qe, 4, T);
+  cols_set(&cp->pre, ym, ye, T, batch);
+  /* a launch that would compute nothing for some item is left whole */
+  const cols_t *all[4] = {&cp->pre, &cp->up0, &cp->up1, &cp->post};
+  for (int k = 0; k < 4; k++)
+    if (all[k]->nq <= 0) return -1;
+  for (int st = 0; st < 2; st++)
+    for (int j = 0; j < 3; j++)
+      for (int br = 0; br < 3; br++)
+        for (int k = 0; k < 2; k++)
+          if (cp->mrf[st][j][br][k].nq <= 0) return -1;
+  cp->on = 1;
+  return 0;
+}
+
+static int cone_enabled(void) {
+  const char *e = getenv("PTD_WINDOW_CONE");
+  return !(e && e[0] == '0');
+}
+
+static void cols_apply(ptk_conv_desc *d, const cols_t *c) {
+  d->q0 = c->q0;
+  d->nq = c->nq;
+  d->ext_l = c->ext_l;
+  d->ext_r = c->ext_r;
+  d->nq_shape = c->nq_shape;
+}
+
+int ptd_window_cols(int64_t T, int batch, int64_t lo_first, int64_t lo, int64_t hi,
+                    int64_t hi_last, int64_t *out) {
+  if (T < 1 || batch < 1 || !out) return -1;
+  const ptk_emit em = {lo_first, lo, hi, hi_last};
+  cone_plan cp;
+  const int on = cone_plan_make(&cp, T, batch, &em) == 0;
+  const int64_t T1 = 4 * T, T2 = 16 * T, L = T2 + 1;
+  const cols_t *seq[PTD_WINDOW_LAUNCHES];
+  cols_t full[PTD_WINDOW_LAUNCHES];
+  int n = 0;
+  seq[n++] = &cp.pre;
+  seq[n++] = &cp.up0;
+  for (int j = 0; j < 3; j++)
+    for (int br = 0; br < 3; br++)
+      for (int k = 0; k < 2; k++) seq[n++] = &cp.mrf[0][j][br][k];
+  seq[n++] = &cp.up1;
+  for (int j = 0; j < 3; j++)
+    for (int br = 0; br < 3; br++)
+      for (int k = 0; k < 2; k++) seq[n++] = &cp.mrf[1][j][br][k];
+  seq[n++] = &cp.post;
+  for (int i = 0; i < n; i++) {
+    if (!on) {   /* the full launches: every column of every item */
+      const int64_t q0 = (i == 1 || i == 20) ? 1 : 0;
+      const int64_t nq = i == 0 ? T : i == 1 ? T + 1 : i < 20 ? T1 : i == 20 ? T1 + 1 : i < 39 ? T2 : L;
+      full[i] = (cols_t){q0, nq, 0, 0, nq};
+      seq[i] = &full[i];
+    }
+    out[5 * i] = seq[i]->q0;
+    out[5 * i + 1] = seq[i]->nq;
+    out[5 * i + 2] = seq[i]->ext_l;
+    out[5 * i + 3] = seq[i]->ext_r;
+    out[5 * i + 4] = seq[i]->nq_shape;
+  }
+  return on;
+}
+
 /* One MRF depth for `batch` items: c1 group then c2 group (see ptd_mrf_depth).  xinL[br]: the
  * LeakyReLU(0.1)'d input of branch br, or NULL to apply the LeakyReLU while staging xin[br];
  * yL: when not NULL, c2 also writes LeakyReLU(0.1) of its output there. */
 static int mrf_depth(pt_ctx *c, const ptd_model *m, int stage, int j, const float *const *xin,
                      const float *const *xinL, float *const *a, float *const *y,
-                     float *const *yL, int64_t T, int batch) {
+                     float *const *yL, int64_t T, int batch, const cols_t (*cols)[2]) {
   const int base = stage == 0 ? 2 : 21, C = stage == 0 ? 256 : 128;
   ptk_conv_desc d1[3], d2[3];
   for (int br = 0; br < 3; br++) {
@@ -244,6 +442,10 @@ static int mrf_depth(pt_ctx *c, const ptd_model *m, int stage, int j, const floa
       d2[br].y2 = yL[br];
       d2[br].a2 = 0.1f;
     }
+    if (cols) {
+      cols_apply(&d1[br], &cols[br][0]);
+      cols_apply(&d2[br], &cols[br][1]);
+    }
   }
   if (ptk_conv_launch(d1, 3, c->g_stream) || ptk_conv_launch(d2, 3, c->g_stream)) {
     PT_LOG("MRF depth %d failed: %s", j, ptk_last_error());
@@ -257,13 +459,14 @@ int ptd_mrf_depth(pt_ctx *c, const ptd_model *m, int stage, int depth, const flo
                   float *const *y_leaky, int64_t T) {
   if (!c || !c->use_cuda || !m || (stage != 0 && stage != 1) || depth < 0 || depth > 2 || T < 1)
     return -1;
-  return mrf_depth(c, m, stage, depth, xin, xin_leaky, a, y, y_leaky, T, 1);
+  return mrf_depth(c, m, stage, depth, xin, xin_leaky, a, y, y_leaky, T, 1, NULL);
 }
 
 /* MRF stack on x [batch][C][T] (xL = LeakyReLU(0.1)(x), or NULL): writes the three branch
  * outputs (before the average) */
 static int mrf_run(pt_ctx *c, const ptd_model *m, int stage, const float *x, const float *xL,
-                   int64_t T, int batch, float *const out[3]) {
+                   int64_t T, int batch, float *const out[3], const cone_plan *cp) {
+  const cols_t(*cols)[3][2] = cp ? cp->mrf[stage] : NULL;
   const int C = stage == 0 ? 256 : 128;
   const size_t tb = (size_t) batch * C * T * sizeof(float);
   float *a[3], *yb[3], *lb[3];
@@ -279,11 +482,12 @@ static int mrf_run(pt_ctx *c, const ptd_model *m, int stage, const float *x, con
   /* depth 0: x -> out[] (+ lb[]); depth 1: out[] -> yb[] (+ lb[], rewritten after depth 1's c1
    * has read it: same stream); depth 2: yb[] -> out[] */
   const float *xs[3] = {x, x, x}, *xls[3] = {xL, xL, xL};
-  if (mrf_depth(c, m, stage, 0, xs, xL ? xls : NULL, a, out, lb, T, batch)) return -1;
+  if (mrf_depth(c, m, stage, 0, xs, xL ? xls : NULL, a, out, lb, T, batch, cols ? cols[0] : NULL))
+    return -1;
   const float *p1[3] = {out[0], out[1], out[2]}, *l1[3] = {lb[0], lb[1], lb[2]};
-  if (mrf_depth(c, m, stage, 1, p1, l1, a, yb, lb, T, batch)) return -1;
+  if (mrf_depth(c, m, stage, 1, p1, l1, a, yb, lb, T, batch, cols ? cols[1] : NULL)) return -1;
   const float *p2[3] = {yb[0], yb[1], yb[2]};
-  return mrf_depth(c, m, stage, 2, p2, l1, a, out, NULL, T, batch);
+  return mrf_depth(c, m, stage, 2, p2, l1, a, out, NULL, T, batch, cols ? cols[2] : NULL);
 }
 
 int ptd_tail(pt_ctx *c, const ptd_model *m, const float *p, int64_t L, int batch, float *wav) {
@@ -323,6 +527,10 @@ static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t ld
   }
   const int64_t T1 = 4 * T, T2 = 16 * T, L = T2 + 1;
   const size_t f = sizeof(float) * (size_t) batch;
+  /* a window that keeps only part of its samples computes only the columns they depend on
+   * (PTD_WINDOW_CONE=0: every column, for comparison) */
+  cone_plan plan, *cp = NULL;
+  if (emit && !stages && cone_enabled() && cone_plan_make(&plan, T, batch, emit) == 0) cp = &plan;
   void *mark = ptdi_arena_mark(c);
   int rc = -1;
   float *h = ptdi_arena_alloc(c, f * 512 * T);
@@ -337,15 +545,17 @@ static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t ld
                  batch);
   d.w16 = m->wr16[0];
   epi_push(&d, PTK_EPI_LEAKY, 0.1f, NULL, 0, 0);
+  if (cp) cols_apply(&d, &cp->pre);
   if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
   /* ups.0 */
   ptdi_convT_desc(&d, h, T, 512 * T, T, 512, m->wr[1], m->b[1], 256, 4, 6, 16, x0, T1, 256 * T1, batch);
   d.w16 = m->wr16[1];
   d.y2 = x0L;
   d.a2 = 0.1f;
+  if (cp) cols_apply(&d, &cp->up0);
   if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
   void *mark1 = ptdi_arena_mark(c);
-  if (mrf_run(c, m, 0, x0, x0L, T1, batch, o0)) goto fail;
+  if (mrf_run(c, m, 0, x0, x0L, T1, batch, o0, cp)) goto fail;
   ptdi_arena_release(c, mark1);   /* the MRF temporaries; o0[] stay */
   float *x1 = ptdi_arena_alloc(c, f * 128 * T2);
   float *x1L = ptdi_arena_alloc(c, f * 128 * T2);
@@ -360,9 +570,10 @@ static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t ld
   d.w16 = m->wr16[20];
   d.y2 = x1L;
   d.a2 = 0.1f;
+  if (cp) cols_apply(&d, &cp->up1);
   if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
   void *mark2 = ptdi_arena_mark(c);
-  if (mrf_run(c, m, 1, x1, x1L, T2, batch, o1)) goto fail;
+  if (mrf_run(c, m, 1, x1, x1L, T2, batch, o1, cp)) goto fail;
   ptdi_arena_release(c, mark2);
   float *p = ptdi_arena_alloc(c, f * 72 * L);
   if (!p) goto oom;
@@ -373,6 +584,7 @@ static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t ld
                  72 * L, L, batch);
   d.w16 = m->wr16[39];
   d.reflect_l1 = 1;
+  if (cp) cols_apply(&d, &cp->post);
   if (ptk_conv_launch(&d, 1, c->g_stream)) goto fail;
   if (ptk_tail_batched(p, L, 72 * L, L, wav, bsw, batch, m->consts, emit, c->g_stream)) goto fail;
   if (stages) {
@@ -442,8 +654,8 @@ int ptd_decode_stages(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, 
   return decode_impl(c, m, z, T, 192 * T, T, 1, wav, 256 * T, NULL, stages);
 }
 
-int ptd_layer(pt_ctx *c, const ptd_model *m, int layer, const float *x, int64_t T, int batch,
-              float *y, float in_leaky, float epi_leaky) {
+static int layer_run(pt_ctx *c, const ptd_model *m, int layer, const float *x, int64_t T, int batch,
+                     float *y, float in_leaky, float epi_leaky, const int64_t *cols) {
   if (!c || !c->use_cuda || !m || layer < 0 || layer >= PTD_DEC_NLAYER - 1 || T < 1 || batch < 1) return -1;
   const layer_geo g = m->g[layer];
   ptk_conv_desc d;
@@ -461,11 +673,26 @@ int ptd_layer(pt_ctx *c, const ptd_model *m, int layer, const float *x, int64_t 
     d.in_a = in_leaky;
   }
   if (epi_leaky > 0.0f) epi_push(&d, PTK_EPI_LEAKY, epi_leaky, NULL, 0, 0);
+  if (cols) {
+    const cols_t cc = {cols[0], cols[1], cols[2], cols[3], cols[4]};
+    cols_apply(&d, &cc);
+  }
   if (ptk_conv_launch(&d, 1, c->g_stream)) {
     PT_LOG("ptd_layer %d failed: %s", layer, ptk_last_error());
     return -1;
   }
   return 0;
+}
+
+int ptd_layer(pt_ctx *c, const ptd_model *m, int layer, const float *x, int64_t T, int batch,
+              float *y, float in_leaky, float epi_leaky) {
+  return layer_run(c, m, layer, x, T, batch, y, in_leaky, epi_leaky, NULL);
+}
+
+int ptd_layer_cols(pt_ctx *c, const ptd_model *m, int layer, const float *x, int64_t T, int batch,
+                   float *y, float in_leaky, float epi_leaky, const int64_t *cols) {
+  if (!cols) return -1;
+  return layer_run(c, m, layer, x, T, batch, y, in_leaky, epi_leaky, cols);
 }
 
 int ptd_mrf(pt_ctx *c, const ptd_model *m, int stage, const float *x, int64_t T, float alpha,
@@ -476,7 +703,7 @@ int ptd_mrf(pt_ctx *c, const ptd_model *m, int stage, const float *x, int64_t T,
   void *mark = ptdi_arena_mark(c);
   float *o[3] = {ptdi_arena_alloc(c, tb), ptdi_arena_alloc(c, tb), ptdi_arena_alloc(c, tb)};
   int rc = -1;
-  if (o[0] && o[1] && o[2] && !mrf_run(c, m, stage, x, NULL, T, 1, o) &&
+  if (o[0] && o[1] && o[2] && !mrf_run(c, m, stage, x, NULL, T, 1, o, NULL) &&
       !ptk_avg3_leaky(o[0], o[1], o[2], out, (int64_t) C * T, alpha, c->g_stream))
     rc = 0;
   else

@@ -27,6 +27,7 @@ int ptk_free(void *p);
 int ptk_h2d_async(void *dst, const void *src, size_t bytes, void *s);
 int ptk_d2h_async(void *dst, const void *src, size_t bytes, void *s);
 int ptk_d2d_async(void *dst, const void *src, size_t bytes, void *s);
+int ptk_fill_async(void *dst, int byte, size_t bytes, void *s);   /* not for captured streams */
 /* row-strided copies: height rows of width_bytes, pitches in bytes */
 int ptk_d2d_2d_async(void *dst, size_t dpitch, const void *src, size_t spitch, size_t width_bytes,
                      size_t height, void *s);
@@ -101,6 +102,14 @@ typedef struct {
   int M;                      /* GEMM rows (cout4 or s*cout4) */
   int C4;                     /* rows per phase (conv: M) */
   int64_t q0, nq;             /* output columns [q0, q0 + nq) */
+  /* Per-item column ranges (overlap-save windows compute only the columns their kept samples
+     depend on): batch item 0 starts ext_l columns earlier, the last item ends ext_r columns
+     later (one item: both).  0, 0: every item computes [q0, q0 + nq). */
+  int64_t ext_l, ext_r;
+  /* columns of one item the tile shape is chosen for (0: nq).  The shape fixes the order in
+     which a column's sums are added, so a launch over a sub-range of columns gives the same bits
+     in those columns as the full launch when it names the full launch's column count here. */
+  int64_t nq_shape;
   /* output */
   float *y;
   float *y2;                  /* optional second output: LeakyReLU(a2) of every value stored in y,

@@ -180,6 +180,10 @@ extern "C" int ptk_d2d_async(void *dst, const void *src, size_t bytes, void *s) 
   if (bytes) HCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t) s));
   return 0;
 }
+extern "C" int ptk_fill_async(void *dst, int byte, size_t bytes, void *s) {
+  HCHK(hipMemsetAsync(dst, byte, bytes, (hipStream_t) s));
+  return 0;
+}
 extern "C" int ptk_d2d_2d_async(void *dst, size_t dpitch, const void *src, size_t spitch,
                                 size_t wb, size_t h, void *s) {
   if (wb && h)
@@ -424,17 +428,22 @@ __device__ __forceinline__ int fdiv(int n, FastDiv f) {
 struct ConvProb {
   int count;                      // workgroups of the problem (grid row blockIdx.y = problem)
   int mt;                         // RB-row blocks
-  int nt;                         // column tiles
-  int rg;                         // row blocks per tile band of the XCD-aware order (0: plain order)
-  FastDiv div_tiles;              // by mt * nt (tiles of one batch item)
+  int nt;                         // column tiles of a middle batch item
+  int nt0;                        // of item 0 (its columns start ext_l earlier; one item: all)
+  int ntl;                        // of the last item (its columns end ext_r later)
+  int nitem;                      // batch items
+  FastDiv div_tiles;              // by mt * nt (tiles of a middle batch item)
   FastDiv div_mt;                 // by mt
   FastDiv div_phase;              // by C4 / RB (row blocks per convT phase) when one_phase
-  int one_phase;                  // every row block lies inside one phase (conv, or C4 % RB == 0)
-  int fast;                       // output / residual index ranges fit the 32-bit epilogue
+  int flags;                      // PROB_ONE_PHASE | PROB_FAST
+  int ext_l;                      // item 0's first column is q0 - ext_l
   int addt;                       // the chain's first tensor add, or -1
   int M;                          // GEMM rows
-  int pad[2];
 };
+// every row block lies inside one phase (conv, or C4 % RB == 0)
+#define PROB_ONE_PHASE 1
+// output / residual index ranges fit the 32-bit epilogue
+#define PROB_FAST 2
 static_assert(sizeof(ConvProb) == 64, "one 64-byte scalar load");
 
 // What the fast epilogue reads, 128 bytes per problem, fetched in one batch of scalar loads when
@@ -444,7 +453,7 @@ struct ConvEpi {
   const float *y, *y2, *t;        // output, its LeakyReLU copy (or null), the residual of op addt
   long long bsy, bst;             // batch strides of y / y2 and of t
   int ldy, ldt;                   // row strides (fit 32 bits on the fast path)
-  int lout, q0, qend, ys, ypad, C4, nepi;
+  int lout, qend, ext_r, ys, ypad, C4, nepi;   // qend: a middle item's column end
   int ops;                        // op e in bits 4e .. 4e + 3
   float a[PTK_MAX_EPI];
   float a2;
@@ -525,33 +534,23 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   // as long as the largest problem's workgroup count, and the excess of a shorter one exits.
   const int p = blockIdx.y;
   const ConvProb pi = g.info[p];
-  int bid = blockIdx.x;
+  const int bid = blockIdx.x;
   if (bid >= pi.count) return;
   const ptk_conv_desc &d = g.d[p];
-  const int mt = pi.mt, nt = pi.nt, rgh = pi.rg;
-  int b, mb, tn;
-  if (rgh > 0) {
-    // XCD-aware order.  Workgroups are handed to the 8 XCDs in turn, so the workgroups of this
-    // problem with the same bid & 7 share one XCD's L2.  Each such set takes one contiguous run
-    // of the tile sequence, and that sequence walks bands of rgh row blocks column by column, so
-    // an XCD's L2 holds a few row blocks of weights and the input columns of its tile run instead
-    // of one row block and every input column.  A bijection on [0, n): the result is unchanged.
-    const int n = pi.count;
-    const int base = n >> 3, rem = n & 7, rho = bid & 7;
-    const int tau = rho * base + (rho < rem ? rho : rem) + (bid >> 3);
-    b = tau / (mt * nt);
-    int r = tau - b * mt * nt;
-    const int band = r / (rgh * nt);
-    r -= band * rgh * nt;
-    const int h = mt - band * rgh < rgh ? mt - band * rgh : rgh;   // the last band may be short
-    tn = r / h;
-    mb = band * rgh + (r - tn * h);
-  } else {
-    b = fdiv(bid, pi.div_tiles);
-    const int r = bid - b * (mt * nt);
-    tn = fdiv(r, pi.div_mt);
-    mb = r - tn * mt;
-  }
+  const int mt = pi.mt;
+  // Tiles item after item, column tile after column tile, row block fastest: item 0 has nt0
+  // column tiles, the middle items nt, the last one ntl >= nt (all nt for a plain launch).
+  // Written as masks and min / max rather than selects, which the compiler turns into branches
+  // around the divisions (measured slower on single-wave-per-SIMD launches).
+  const int c0 = mt * pi.nt0, t = bid - c0;
+  const int past0 = ~(t >> 31);                          // -1 past item 0's tiles, else 0
+  const int bq = fdiv(max(t, 0), pi.div_tiles);
+  const int b = min(bq + 1, pi.nitem - 1) & past0;      // the last item takes its extra tiles
+  const int r = bid - ((c0 + (b - 1) * (mt * pi.nt)) & past0);
+  const int tn = fdiv(r, pi.div_mt);
+  const int mb = r - tn * mt;
+  const bool last_item = b == pi.nitem - 1;
+  const long long q0i = d.q0 - (long long) (pi.ext_l & ~past0);   // this item's first column
   const int S = g.split, lgS = g.lg_split, G = 4 >> lgS;
 
   // descriptor fields used in loops, read once (the problem index is dynamic, so the compiler
@@ -571,19 +570,21 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   // The phase of this row block (convT: row m is phase m / C4 of channel m % C4), when the block
   // lies inside one phase.
   const bool phase_rows = d.C4 != d.M;
-  const bool one_phase = pi.one_phase != 0;
+  const bool one_phase = (pi.flags & PROB_ONE_PHASE) != 0;
   const int r_tile = phase_rows && one_phase ? fdiv(mb, pi.div_phase) : 0;
   // Lane l < RB loads the bias of the block's row l once the first chunk's loads are in flight,
   // and the epilogue fetches each value's bias from the lane of its row (ds_bpermute): the load's
   // latency is spent behind the main loop, and no wave depends on another's write.
   float bias_r = 0.0f;
   auto load_bias = [&]() {
-    if (lane < RB) {
-      const int m = mb * RB + lane;
-      int co = m;
-      if (phase_rows) co = one_phase ? m - r_tile * d.C4 : m % d.C4;
-      if (d.bias != nullptr && m < d.M && co < d.nbias) bias_r = d.bias[co];
-    }
+    // the fields read in one batch ahead of any branch (under the kernel's scalar-register
+    // pressure the compiler re-reads kernel arguments where they are used, one wait per read)
+    const float *bp = d.bias;
+    const int nbias = d.nbias, Mr = d.M, C4r = d.C4;
+    const int m = mb * RB + lane;
+    int co = m - r_tile * C4r;   // conv: r_tile = 0
+    if (!one_phase) co = m % C4r;
+    if (lane < RB && bp != nullptr && m < Mr && co < nbias) bias_r = bp[co];
   };
   // bias of row `row` of the block (every lane of the wave must be active)
   auto bias_of = [&](int row) {
@@ -593,8 +594,8 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   const int l32 = lane & 31;
   const int quad = lane >> 4;     // RB = 16: the reduction index (and row group) of this lane
   const int l16 = lane & 15;
-  const int q0off = (tn * G + cg) * (32 * NB);   // this wave's first column past d.q0
-  const long long q0 = d.q0 + q0off;
+  const int q0off = (tn * G + cg) * (32 * NB);   // this wave's first column past the item's first
+  const long long q0 = q0i + q0off;
   const int kd = (K - 1) * dil;
   const int dmin = kd < 0 ? kd : 0;
   const int XW = (32 * NB - 1) * st + (kd < 0 ? -kd : kd) + 1;
@@ -798,7 +799,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   // nb, the 16 values v of column q0 + 32*nb + l32 at rows 8*(v >> 2) + 4*half + (v & 3) of the
   // block.  RB = 16: lane (l16, quad) holds 8 values v of column q0 + 32*nb + 16*(v >> 2) + l16 at
   // rows 4*quad + (v & 3).  Wave ks of a column group finishes v in [v0, v0 + NV/S).
-  const long long qend = d.q0 + d.nq;
+  const long long qend = d.q0 + d.nq + (last_item ? d.ext_r : 0);
   const int M = d.M, C4 = d.C4, ys = d.ys, ypad = d.ypad, nepi = d.nepi;
   const long long Lout = d.Lout, ldy = d.ldy;
   float *yb = d.y + (long long) b * d.bsy;
@@ -848,7 +849,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   // in bounds without a branch (a lane whose column does not exist stores nothing).  The values
   // of a lane are val[i], i < nv: value v0 + i of the block.  The chain runs op by op over all of
   // them, one branch per op.
-  if (pi.fast && one_phase && mb * RB + RB <= pi.M) {
+  if ((pi.flags & PROB_FAST) && one_phase && mb * RB + RB <= pi.M) {
     const ConvEpi ep = g.ep[p];
     constexpr int NMAX = RB == 32 ? 16 : 8;
     // values come in groups of GRP that a wave finishes together (nv is a multiple of GRP)
@@ -868,6 +869,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
     // lane part of the row of value i, and its wave-uniform part
     const int lrow = RB == 32 ? 4 * half : 4 * quad;
     auto urow = [&](int i) { return RB == 32 ? 8 * (((v0 + i) >> 2)) + ((v0 + i) & 3) : ((v0 + i) & 3); };
+    const int qend32 = ep.qend + (last_item ? ep.ext_r : 0);
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) {
       // columns of this lane: one per column block (RB = 32), two (RB = 16)
@@ -875,9 +877,9 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
       int cl[NCB];
 #pragma unroll
       for (int cb = 0; cb < NCB; cb++) {
-        const int q = ep.q0 + q0off + 32 * nb + (RB == 32 ? l32 : 16 * cb + l16);
+        const int q = (int) q0 + 32 * nb + (RB == 32 ? l32 : 16 * cb + l16);
         const int col = q * ep.ys + r_tile - ep.ypad;
-        ok[cb] = q < ep.qend && col >= 0 && col < ep.lout;
+        ok[cb] = q < qend32 && col >= 0 && col < ep.lout;
         cl[cb] = ok[cb] ? col : 0;
       }
       auto cbo = [&](int i) { return RB == 32 ? 0 : ((v0 + i) >> 2); };
@@ -1010,10 +1012,6 @@ static int env_knob(const char *name) {
   const char *e = getenv(name);
   return e ? atoi(e) : 0;
 }
-static int env_knob_or(const char *name, int dflt) {
-  const char *e = getenv(name);
-  return e ? atoi(e) : dflt;
-}
 
 // Tile shape (RB rows, channel split S in {1, 2, 4}; PTK_CONV_RB and PTK_CONV_SPLIT override).
 // All waves of a launch usually fit on the chip at once, so a launch lasts as long as its busiest
@@ -1024,9 +1022,10 @@ static int env_knob_or(const char *name, int dflt) {
 // and 22, C 128 / 256, K 3-11), picks the shape with the best predicted MFMA occupancy:
 //   eff = [mean / max waves per SIMD] x [latency hiding at the mean] x [split cost]
 //         x [rows that exist / rows computed] x [16-row tile cost]
-// evaluated on ONE batch item's grid.  The shape fixes the order in which a block's partial sums
-// are added, so choosing it without the batch size makes a batched item's result bit-identical to
-// the same item decoded alone (and it measured faster at batch 8 than a batch-aware choice).
+// evaluated on ONE batch item's grid (of nq_shape columns when the launch covers a sub-range).
+// The shape fixes the order in which a block's partial sums are added, so choosing it without the
+// batch size makes a batched item's result bit-identical to the same item decoded alone (and it
+// measured faster at batch 8 than a batch-aware choice).
 // 16-row tiles double the waves of a grid (and cut the padding of row counts like 72), at twice
 // the window staging and epilogue work per MFMA.  They need the 16-row weight copy (w16) and are
 // offered to single-problem launches only (PTK_CONV_RB=16 forces them on any launch with the
@@ -1063,10 +1062,11 @@ static int choose_tiles(const ptk_conv_desc *const *ds, int n, int nb, int *rb_o
       double rows = 0.0, rows_run = 0.0;
       for (int i = 0; i < n; i++) {
         const ptk_conv_desc *d = ds[i];
+        const long long nq = d->nq_shape > 0 ? d->nq_shape : d->nq;
         const long long mt = (d->M + RB - 1) / RB;
-        const long long tiles = mt * ((d->nq + 32LL * nb * G - 1) / (32LL * nb * G));
+        const long long tiles = mt * ((nq + 32LL * nb * G - 1) / (32LL * nb * G));
         waves += 4LL * tiles;
-        const double work = (double) d->nq * d->K * d->cinp;
+        const double work = (double) nq * d->K * d->cinp;
         rows += work * d->M;
         rows_run += work * (double) (mt * RB);
       }
@@ -1080,30 +1080,6 @@ static int choose_tiles(const ptk_conv_desc *const *ds, int n, int nb, int *rb_o
     }
   }
   *rb_out = best_rb;
-  return best;
-}
-
-// Band height of the XCD-aware tile order: each XCD runs about n / 8 consecutive tiles of the
-// band sequence, R row blocks x (n / 8) / R column tiles, and its L2 fetches R row blocks of
-// weights (rb rows x cin x K) plus (n / 8) / R input column windows (cin x the window width).
-// R is the power of two (up to the row blocks of a batch item) that minimises that sum.  When an
-// XCD's run covers a whole batch item or more, R = all rows (bands do not matter then).
-static int xcd_band(const ptk_conv_desc *d, int rb, int mt, int nt, int cols_per_tile) {
-  const long long tiles = (long long) mt * nt;
-  const long long q = (tiles * d->batch + 7) / 8;
-  if (q >= tiles) return mt;
-  const int kd = (d->K - 1) * d->dil;
-  const double wrow = (double) rb * d->cinp * d->K;
-  const double xcol = (double) d->cin * ((double) cols_per_tile * d->stride + (kd < 0 ? -kd : kd));
-  int best = 1;
-  double best_cost = -1.0;
-  for (int R = 1; R <= mt; R *= 2) {
-    const double cost = R * wrow + (double) ((q + R - 1) / R) * xcol;
-    if (best_cost < 0.0 || cost < best_cost) {
-      best_cost = cost;
-      best = R;
-    }
-  }
   return best;
 }
 
@@ -1175,6 +1151,11 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
       return -1;
     }
     if (d->nq <= 0 || d->batch <= 0) continue;
+    if (d->ext_l < 0 || d->ext_r < 0 || d->nq_shape < 0 || d->ext_l >= (1LL << 30) ||
+        d->ext_r >= (1LL << 30)) {
+      set_err("ptk_conv_launch: column extension or shape width out of range");
+      return -1;
+    }
     // a row tile's weight panel is addressed through one buffer resource (the input rows are
     // bounded the same way by ptk_conv_mfma_ok)
     if ((unsigned long long) d->K * (unsigned long long) (d->cinp / CONV_CK) * 1024ull >= (unsigned long long) PTK_OOB) {
@@ -1201,17 +1182,22 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
   const int S = choose_tiles(live, g.ngroup, nb, &rb), G = 4 / S;
   g.split = S;
   g.lg_split = S == 4 ? 2 : S == 2 ? 1 : 0;
-  // XCD-aware tile order: opt-in (PTK_XCD_MAP=1).  On the dominant MRF launch it cuts the L2
-  // fills by 15 % (FETCH_SIZE 28.7 -> 24.4 MB) but did not make any decoder shape faster: those
-  // fills mostly hit the MALL and the launch is bound by MFMA time and its fixed edges.
-  const int xcd_map = env_knob_or("PTK_XCD_MAP", 0);
   for (int i = 0; i < g.ngroup; i++) {
     const ptk_conv_desc *d = live[i];
     ConvProb &pi = g.info[i];
+    const long long cols = 32LL * nb * G;   // columns of one tile
     pi.mt = (d->M + rb - 1) / rb;
-    pi.nt = (int) ((d->nq + 32LL * nb * G - 1) / (32LL * nb * G));
-    pi.rg = xcd_map ? xcd_band(d, rb, pi.mt, pi.nt, 32 * nb * G) : 0;
-    const long long n = (long long) pi.mt * pi.nt * d->batch;
+    pi.nt = (int) ((d->nq + cols - 1) / cols);
+    pi.nitem = d->batch;
+    long long n;
+    if (d->batch == 1) {
+      pi.nt0 = pi.ntl = (int) ((d->nq + d->ext_l + d->ext_r + cols - 1) / cols);
+      n = (long long) pi.mt * pi.nt0;
+    } else {
+      pi.nt0 = (int) ((d->nq + d->ext_l + cols - 1) / cols);
+      pi.ntl = (int) ((d->nq + d->ext_r + cols - 1) / cols);
+      n = (long long) pi.mt * (pi.nt0 + (long long) (d->batch - 2) * pi.nt + pi.ntl);
+    }
     if (n >= (1LL << 24) || total + n >= (1LL << 31)) {
       set_err("ptk_conv_launch: %lld workgroups for one problem (the tile decode takes < 2^24)", n);
       return -1;
@@ -1221,7 +1207,7 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
     if (pi.count > maxcount) maxcount = pi.count;
     pi.div_tiles = fast_div((unsigned) (pi.mt * pi.nt));
     pi.div_mt = fast_div((unsigned) pi.mt);
-    pi.one_phase = d->C4 == d->M || d->C4 % rb == 0;
+    const bool one_phase = d->C4 == d->M || d->C4 % rb == 0;
     pi.div_phase = fast_div(d->C4 == d->M ? 1u : (unsigned) (d->C4 / rb > 0 ? d->C4 / rb : 1));
     pi.addt = -1;
     for (int e = 0; e < d->nepi; e++)
@@ -1229,14 +1215,15 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
     pi.M = d->M;
     // the fast epilogue's 32-bit indices: columns, and byte offsets from a row block's first row
     const long long lim31 = 1LL << 31, lim30 = 1LL << 30;
-    bool fast = pi.one_phase && d->ldy < (1LL << 23) && d->Lout < lim30 &&
-                (d->q0 + d->nq) * d->ys + d->C4 < lim30 && d->q0 >= 0 &&
+    bool fast = one_phase && d->ldy < (1LL << 23) && d->Lout < lim30 &&
+                (d->q0 + d->nq + d->ext_r) * d->ys + d->C4 < lim30 && d->q0 - d->ext_l >= 0 &&
                 ((long long) rb * d->ldy + d->Lout) * 4 < lim31;
     if (pi.addt >= 0) {
       const long long ldt = d->epi[pi.addt].ldt;
       fast = fast && ldt >= 0 && ldt < (1LL << 23) && ((long long) rb * ldt + d->Lout) * 4 < lim31;
     }
-    pi.fast = fast;
+    pi.flags = (one_phase ? PROB_ONE_PHASE : 0) | (fast ? PROB_FAST : 0);
+    pi.ext_l = (int) d->ext_l;
     ConvEpi &ep = g.ep[i];
     ep.y = d->y;
     ep.y2 = d->y2;
@@ -1246,8 +1233,8 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
     ep.ldy = (int) d->ldy;
     ep.ldt = pi.addt >= 0 ? (int) d->epi[pi.addt].ldt : 0;
     ep.lout = (int) d->Lout;
-    ep.q0 = (int) d->q0;
     ep.qend = (int) (d->q0 + d->nq);
+    ep.ext_r = (int) d->ext_r;
     ep.ys = d->ys;
     ep.ypad = d->ypad;
     ep.C4 = d->C4;

@@ -229,23 +229,53 @@ def test_batched_decode_matches_single(env, T, batch):
     dz.free(); dw.free()
 
 
-@pytest.mark.gpu
-@pytest.mark.parametrize("T,batch", [(226, 1), (97, 3)])
-def test_xcd_tile_order_same_result(env, T, batch, monkeypatch):
-    """The opt-in XCD-aware tile order (PTK_XCD_MAP=1) only permutes which workgroup computes
-    which tile: the waveform is bit-identical to the plain order's."""
+# (layer, T, cols relative to the full launch: q0 offset, nq, ext_l, ext_r)
+LAYER_COLS = [(0, 150, 20, 70, 13, 31), (1, 60, 9, 33, 5, 17), (20, 90, 30, 41, 29, 2),
+              (18, 300, 37, 151, 36, 100), (37, 200, 100, 1, 99, 99), (38, 130, 1, 64, 0, 0),
+              (39, 257, 64, 128, 40, 65)]
+
+
+@pytest.mark.parametrize("rb,split", [(0, 0), (16, 1), (32, 2), (32, 4), (16, 4)])
+def test_layer_cols_per_item(env, rb, split, monkeypatch):
+    """A launch over part of the columns (the windowed decode's form: middle items [q0, q0 + nq),
+    item 0 from ext_l earlier, the last item to ext_r later, tile shape of the full width) writes
+    exactly those columns of each item, bit-identical to the full launch, and nothing else: conv
+    and both convT layers, an MRF K = 11 conv at dilation 5, conv_post; batches 1, 2 and 3; every
+    tile shape (rb, split 0: the launcher's choice)."""
     ctx, model, ws, bs = env
-    say(f"xcd tile order T={T} batch={batch}")
-    dz = dev_of(ctx, np.stack([synth.latent(T, 700 + i) for i in range(batch)]))
-    dw = pkg.DevBuf(batch * 256 * T)
-    outs = []
-    for flag in ("0", "1"):
-        monkeypatch.setenv("PTK_XCD_MAP", flag)
-        assert ctx.lib.ptd_decode(ctx.ptr, model.ptr, dz.ptr, T, batch, dw.ptr) == 0
-        outs.append(dw.download(ctx))
-    monkeypatch.delenv("PTK_XCD_MAP")
-    assert np.array_equal(outs[0], outs[1])
-    dz.free(); dw.free()
+    say(f"layer columns rb={rb} split={split}")
+    if rb:
+        monkeypatch.setenv("PTK_CONV_RB", str(rb))
+        monkeypatch.setenv("PTK_CONV_SPLIT", str(split))
+    lib = ctx.lib
+    rng = np.random.default_rng(rb * 10 + split)
+    for layer, T, off, nq, el, er in LAYER_COLS:
+        g = synth.dec_layer(layer)
+        cin, cout4 = g["cin"], (g["cout"] + 3) // 4 * 4
+        convT = g["convT"]
+        Tout = 4 * T if convT else T
+        q_full0, nq_full = (1, T + 1) if convT else (0, T)
+        for batch in (1, 2, 3):
+            x = rng.standard_normal((batch, cin, T)).astype(np.float32)
+            dx = dev_of(ctx, x)
+            sentinel = np.float32(-12345.5)
+            dfull = pkg.DevBuf(batch * cout4 * Tout)
+            assert lib.ptd_layer(ctx.ptr, model.ptr, layer, dx.ptr, T, batch, dfull.ptr, 0.1, 0.1) == 0
+            full = dfull.download(ctx).reshape(batch, cout4, Tout)
+            dy = pkg.DevBuf.of(ctx, np.full(batch * cout4 * Tout, sentinel, np.float32))
+            q0 = q_full0 + off
+            cols = (C.c_int64 * 5)(q0, nq, el, er, nq_full)
+            assert lib.ptd_layer_cols(ctx.ptr, model.ptr, layer, dx.ptr, T, batch, dy.ptr, 0.1, 0.1,
+                                      cols) == 0
+            y = dy.download(ctx).reshape(batch, cout4, Tout)
+            for b in range(batch):
+                a = q0 - el if b == 0 else q0
+                e = q0 + nq + er if b == batch - 1 else q0 + nq
+                lo, hi = (max(4 * a - 6, 0), min(4 * e - 6, Tout)) if convT else (a, e)
+                assert np.array_equal(y[b, :, lo:hi], full[b, :, lo:hi]), (layer, batch, b)
+                assert np.all(y[b, :, :lo] == sentinel) and np.all(y[b, :, hi:] == sentinel), \
+                    (layer, batch, b)
+            dx.free(); dfull.free(); dy.free()
 
 
 @pytest.mark.parametrize("rb,split", [(16, 1), (16, 2), (16, 4), (32, 1), (32, 2), (32, 4)])
@@ -352,6 +382,7 @@ def test_windows_schedule_edges_bitexact(env, T, win, cx):
             break
         a = max(e1 - cx, 1)
     dz, dw = dev_of(ctx, z), pkg.DevBuf.of(ctx, np.full(256 * T, np.nan, np.float32))
+    assert ctx.lib.ptd_debug_fill_arena(ctx.ptr, 0xFF) == 0   # columns never written read as NaN
     assert ctx.lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, win, cx, dw.ptr) == 0
     wav = dw.download(ctx)
     assert np.array_equal(wav, ref), f"max diff {np.nanmax(np.abs(wav - ref))}"
@@ -369,6 +400,29 @@ def test_config5_longform_windows_vs_full(env):
     assert ctx.lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, 96, 16, dw.ptr) == 0
     wav = dw.download(ctx)
     assert np_ref.sndr(wav, full) >= 60.0
+    dz.free(); dw.free()
+
+
+@pytest.mark.parametrize("T,win,cx", [(1500, 96, 16), (777, 96, 16), (400, 48, 16)])
+def test_window_columns_change_no_sample(env, T, win, cx, monkeypatch):
+    """The windowed decode computes only the columns its kept samples depend on: with the arena
+    poisoned (every column it leaves out reads NaN) its output is bit-identical to the same decode
+    computing every column (PTD_WINDOW_CONE=0), at config 5's long-form shape and two others."""
+    ctx, model, ws, bs = env
+    say(f"window columns T={T} win={win} ctx={cx}")
+    lib = ctx.lib
+    z = synth.latent(T, 900 + T)
+    dz, dw = dev_of(ctx, z), pkg.DevBuf(256 * T)
+    monkeypatch.setenv("PTD_WINDOW_CONE", "0")
+    assert lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, win, cx, dw.ptr) == 0
+    whole = dw.download(ctx)
+    monkeypatch.delenv("PTD_WINDOW_CONE")
+    dw.upload(ctx, np.full(256 * T, np.nan, np.float32))
+    assert lib.ptd_debug_fill_arena(ctx.ptr, 0xFF) == 0
+    assert lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, win, cx, dw.ptr) == 0
+    wav = dw.download(ctx)
+    assert np.all(np.isfinite(wav))
+    assert np.array_equal(wav, whole)
     dz.free(); dw.free()
 
 
@@ -402,6 +456,7 @@ def test_stream_chunks_stitched_equal_windows(env, T, win, cx):
         a += step
     stitched = np.concatenate(out)
     dw = pkg.DevBuf(256 * T)
+    assert lib.ptd_debug_fill_arena(ctx.ptr, 0xFF) == 0   # columns never written read as NaN
     assert lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, win, cx, dw.ptr) == 0
     wav = dw.download(ctx)
     assert stitched.shape == wav.shape

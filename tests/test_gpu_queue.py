@@ -93,6 +93,7 @@ def test_windows2_matches_the_reference_stream_loop(env, T, wf, w, cx):
     assert lib.ptd_windows2_arena_bytes(T, wf, w, cx) <= 1024 << 20
     dz, dw = pkg.DevBuf.of(ctx, z), pkg.DevBuf(HOP * T)
     dw.upload(ctx, np.full(HOP * T, np.nan, np.float32))
+    assert lib.ptd_debug_fill_arena(ctx.ptr, 0xFF) == 0   # columns never written read as NaN
     assert lib.ptd_decode_windows2(ctx.ptr, model.ptr, dz.ptr, T, wf, w, cx, dw.ptr) == 0
     got = dw.download(ctx)
     dz.free(); dw.free()
