@@ -482,13 +482,16 @@ def main():
                 raise RuntimeError("mrf depth failed")
         ctx.sync()
         log(f"kernel loop: {2 * args.kernel_loop} launches done")
-        # the narrow late stages: the fused tail kernel at config 4's shape, as many launches
-        tp, tw = tail_setup(pkg, ctx, TAIL_L, 1)
-        for _ in range(args.kernel_loop):
-            if lib.ptd_tail(ctx.ptr, model.ptr, tp.ptr, TAIL_L, 1, tw.ptr) != 0:
-                raise RuntimeError("tail failed")
-        ctx.sync()
-        log(f"kernel loop: {args.kernel_loop} tail launches (L {TAIL_L}) done")
+        # the narrow late stages: the fused tail kernel at config 4's shape, as many launches of
+        # one request and of 64 requests at once (256- and 1024-sample tiles)
+        for tb in (1, 64):
+            tp, tw = tail_setup(pkg, ctx, TAIL_L, tb)
+            for _ in range(args.kernel_loop):
+                if lib.ptd_tail(ctx.ptr, model.ptr, tp.ptr, TAIL_L, tb, tw.ptr) != 0:
+                    raise RuntimeError("tail failed")
+            ctx.sync()
+            tp.free(); tw.free()
+            log(f"kernel loop: {args.kernel_loop} tail launches (L {TAIL_L}, batch {tb}) done")
         # calibration for the HBM byte counters: add_kernel over 64 Mi floats reads exactly
         # 512 MiB and writes 256 MiB per launch
         n = 64 << 20

@@ -16,7 +16,9 @@
 
 #include <type_traits>
 
+#include <limits.h>
 #include <math.h>
+#include <stdint.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -1454,184 +1456,235 @@ extern "C" int ptk_leaky(const float *a, float *y, int64_t n, float alpha, void 
 //   frame[b][n][t] = hann[n] * sum_k (re Bc[k][n] + im Bs[k][n]),  re/im = exp(p_k) cos/sin(pi sin(p_9+k))
 //   ola[b][j] = sum_{j-4t in [0,16)} frame[b][j-4t][t];   y[b][i] = ola[b][i+8] / max(wsum[i+8], 1e-9)
 //   wav[o] = sum_b sum_m h[b][m] * 4 * y[b][(o+m-31)/4]   over (o+m-31) = 0 mod 4 in range.
-// One workgroup of TAIL_THREADS threads produces TAIL_OUT consecutive samples; it recomputes the
-// ~TAIL_OUT/16 + 5 frames per band it needs (in LDS), so the whole tail is a single pass over p
-// with no intermediates.  Every sample is computed by the same operations whatever the block
-// size, so the launcher picks the size from the grid without changing a result.
-#define TAIL_KP 12   // a frame's 9 spectrum values padded to 12: three aligned float4 reads
+// A tile is TOUT consecutive samples of one item, made by one workgroup of four waves that
+// recomputes the frames the tile needs, so the whole tail is a single pass over p with no
+// intermediates in HBM.  Its two products run on the fp32 16x16x4 MFMA (lane l holds A[l%16][l/16],
+// B[l/16][l%16] and result rows 4(l/16)+i of column l%16):
+//   - the irfft: 16 frames x 16 samples per product group, the spectrum as A (k = the lane's bin
+//     group: re of bin g, im of bin g (bin 0's k group carries re of bin 8 instead: the imaginary
+//     parts of bins 0 and 8 meet sin(0) and sin(pi n), which vanish), re and im of bin g + 4), the
+//     basis with hann folded in as B;
+//   - the PQMF synthesis: samples o0' + 16m + 4q + r of a 256-sample block are
+//     sum_b sum_s y_b[64k + 4m + 1 + s] * 4 h_b[3 - r + 4(s - q)], a Hankel product over the 19
+//     shifts s with the four bands as the k of each MFMA.
+// Wave w makes band w's frames and y values (phases A and B touch only that wave's LDS, so they
+// need no barrier), then the waves make one 256-sample block each from all bands' y (phase C).
+// A workgroup loops over tiles (tile, tile + gridDim.x, ...); the next tile's reads are issued as
+// soon as the current tile's are used and arrive while phases B and C run.
+template <int TOUT>
+struct TailGeo {
+  static constexpr int NG = ((TOUT / 4 + 27) / 4 + 16) / 16;   // 16-frame groups per band
+  static constexpr int P = 64 * NG + 32;     // one overlap-add plane (floats); a multiple of 32
+  static constexpr int SLOTS = TOUT / 4 + 16;  // y slots per band: slot u + 1 + j for u < TOUT/4
+  static constexpr int YP = TOUT / 4 + 20;   // a band's y row: slot at +3, read 20 at a time
+  static constexpr int NB = TOUT / 256;      // 256-sample output blocks
+};
 
-template <int TAIL_OUT, int TAIL_THREADS>
-__global__ void __launch_bounds__(TAIL_THREADS) tail_kernel(const float *__restrict__ p, long long ldp,
-                                                        long long bsp, long long L,
-                                                        float *__restrict__ wav, long long bsw,
-                                                        const float *__restrict__ cst, ptk_emit em) {
-  constexpr int TAIL_NY = TAIL_OUT / 4 + 18, TAIL_NT = TAIL_NY / 4 + 6;
-  static_assert(TAIL_OUT / 4 <= TAIL_THREADS && TAIL_THREADS % 16 == 0, "phase 2 / 4 thread maps");
-  // samples of this item that are kept; a block entirely outside them does no work
-  const long long e_lo = blockIdx.y == 0 ? em.lo_first : em.lo;
-  const long long e_hi = blockIdx.y + 1 == gridDim.y ? em.hi_last : em.hi;
-  if ((long long) blockIdx.x * TAIL_OUT >= e_hi || ((long long) blockIdx.x + 1) * TAIL_OUT <= e_lo) return;
-  // the spectra (phases 1-2) and the y rows (phases 3-4) are never live together: y reuses the
-  // spectra's LDS, which keeps three 1024-sample blocks resident per CU
-  constexpr int SPEC = 2 * 4 * TAIL_NT * TAIL_KP;
-  static_assert(4 * TAIL_NY <= SPEC, "y fits over the spectra");
-  __shared__ __align__(16) float s_spec[SPEC];
-  __shared__ __align__(16) float s_fr[4][TAIL_NT][16];
-  auto s_re = reinterpret_cast<float (*)[TAIL_NT][TAIL_KP]>(s_spec);
-  auto s_im = reinterpret_cast<float (*)[TAIL_NT][TAIL_KP]>(s_spec + 4 * TAIL_NT * TAIL_KP);
-  auto s_y = reinterpret_cast<float (*)[TAIL_NY]>(s_spec);
-  __shared__ float s_hann[16];
-  const int tid = threadIdx.x;
+template <int TOUT>
+__global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, long long ldp,
+                                                   long long bsp, int L, float *__restrict__ wav,
+                                                   long long bsw, const float *__restrict__ cst,
+                                                   ptk_emit em, int nbx, int ntiles) {
+  using G = TailGeo<TOUT>;
+  constexpr int NG = G::NG, P = G::P, SLOTS = G::SLOTS, YP = G::YP, NB = G::NB;
+  static_assert(NB >= 1 && NB <= 4 && TOUT % 256 == 0, "one 256-sample block per wave");
+  // s_pl[band][jt][jr]: sample n = 4 jt + (jr & 3) of relative frame (jr >> 2) - jt, so
+  // ola[jr] = sum_jt s_pl[band][jt][jr]; s_y[band][slot + 3]
+  __shared__ __align__(16) float s_pl[4 * 4 * P];
+  __shared__ __align__(16) float s_y[4 * YP];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int lm = lane & 15, lg = lane >> 4;
   const float *hann = cst, *bc = cst + 16, *bs = cst + 160, *hp = cst + 304, *hb = cst + 560;
-  if (tid < 16) s_hann[tid] = hann[tid];
-  // the basis column of this thread's phase-2 sample, loaded while phase 1 runs
-  const int n2 = tid & 15, g2 = tid >> 4;
-  float cb[9], sb[9];
-#pragma unroll
-  for (int k = 0; k < 9; k++) {
-    cb[k] = bc[k * 16 + n2];
-    sb[k] = bs[k * 16 + n2];
-  }
-  const float hn = hann[n2];
-  const long long Ly = 4 * (L - 1);
-  const long long nout = 4 * Ly;
-  const long long o0 = (long long) blockIdx.x * TAIL_OUT;
-  p += (long long) blockIdx.y * bsp;
-  wav += (long long) blockIdx.y * bsw;
-  // y indices this block needs: i = (o + m - 31) / 4 for o in [o0, o0+TAIL_OUT), m in [0, 63);
-  // >> 2 on a signed value is floor division by 4, also below zero
-  const long long i_lo = (o0 - 31) >> 2;
-  // frames t needed by ola index j = i + 8 >= i_lo + 8: 4t in [j - 15, j]
-  const long long t_lo = (i_lo - 4) >> 2;
-  // 1) spectra of the needed frames: element e = row * TAIL_NT + frame over all threads (row =
-  //    band * 9 + bin), so consecutive threads read consecutive frames of a row (coalesced).  All
-  //    of a thread's reads are issued before any of them is used.
-  constexpr int NSP = 36 * TAIL_NT, NIT1 = (NSP + TAIL_THREADS - 1) / TAIL_THREADS;
-  float lm[NIT1], lph[NIT1];
-#pragma unroll
-  for (int it = 0; it < NIT1; it++) {
-    const int e = tid + it * TAIL_THREADS;
-    const int row = e / TAIL_NT, tt = e - row * TAIL_NT, b = row / 9, k = row - 9 * b;
-    const long long t = t_lo + tt;
-    lm[it] = lph[it] = 0.0f;
-    if (e < NSP && t >= 0 && t < L) {
-      lm[it] = p[(long long) (b * 18 + k) * ldp + t];
-      lph[it] = p[(long long) (b * 18 + 9 + k) * ldp + t];
+  const int Ly = 4 * (L - 1), nout = 4 * Ly;
+  const int batch = ntiles / nbx;
+
+  // the next tile at or after t (stepping by the grid) that holds samples of its item to keep
+  auto next_kept = [&](int t) {
+    for (; t < ntiles; t += (int) gridDim.x) {
+      const int item = t / nbx;
+      const long long o0 = (long long) (t - item * nbx) * TOUT;
+      const long long e_lo = item == 0 ? em.lo_first : em.lo;
+      const long long e_hi = item + 1 == batch ? em.hi_last : em.hi;
+      if (o0 < e_hi && o0 + TOUT > e_lo) break;
     }
-  }
+    return t;
+  };
+  int tile = next_kept((int) blockIdx.x);
+  if (tile >= ntiles) return;
+
+  // reads of one tile: for frame group c of band w, lane (m, g) reads frame t_lo + 16c + m of
+  // bins g and g + 4 (magnitude and phase) and, in k group 0, bin 8.  The item's 72 rows are one
+  // buffer; a frame outside [0, L) gets an offset past it and reads 0 (the host keeps 72 * ldp
+  // floats within 2 GiB); the row steps between the reads are scalar offsets.
+  const unsigned nrec = (unsigned) (72 * ldp * 4), ldp4 = (unsigned) (ldp * 4);
+  const unsigned ro = (unsigned) (18 * w + lg) * ldp4;
+  float ld[NG][6];
+  auto issue = [&](int t) {
+    const int item = t / nbx;
+    const int t_lo = (t - item * nbx) * (TOUT / 16) - 3;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        (void *) (p + (long long) item * bsp), (short) 0, (int) nrec, PTK_BUF_WORD3);
 #pragma unroll
-  for (int it = 0; it < NIT1; it++) {
-    const int e = tid + it * TAIL_THREADS;
-    const int row = e / TAIL_NT, tt = e - row * TAIL_NT, b = row / 9, k = row - 9 * b;
-    const long long t = t_lo + tt;
-    if (e < NSP) {
-      float re = 0.0f, im = 0.0f;
-      if (t >= 0 && t < L) {
-        // the hardware transcendentals: v_exp_f32 is 2^x, v_sin_f32 / v_cos_f32 take revolutions
-        // (sin(2 pi x)).  The phase pi * sin(p) in revolutions is sin(p) / 2, within [-1/2, 1/2],
-        // so no range reduction is needed; p itself is a conv output of modest size.
-        const float mag = __builtin_amdgcn_exp2f(lm[it] * 1.44269504f);
-        const float rev = 0.5f * __builtin_amdgcn_sinf(lph[it] * 0.159154943f);
-        re = mag * __builtin_amdgcn_cosf(rev);
-        im = mag * __builtin_amdgcn_sinf(rev);
-      }
-      s_re[b][tt][k] = re;
-      s_im[b][tt][k] = im;
+    for (int c = 0; c < NG; c++) {
+      const int tf = t_lo + 16 * c + lm;
+      const bool ok = (unsigned) tf < (unsigned) L;
+      const unsigned vo = ok ? ro + (unsigned) tf * 4u : PTK_OOB;
+      const unsigned vo8 = ok && lg == 0 ? vo + 8u * ldp4 : PTK_OOB;
+      ld[c][0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, vo, 0, 0));
+      ld[c][1] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, vo, 9 * ldp4, 0));
+      ld[c][2] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, vo, 4 * ldp4, 0));
+      ld[c][3] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, vo, 13 * ldp4, 0));
+      ld[c][4] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, vo8, 0, 0));
+      ld[c][5] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, vo8, 9 * ldp4, 0));
     }
-  }
-  __syncthreads();
-  // 2) windowed frames (irfft through the basis): thread (n, g) owns sample n of frames g, g + 32,
-  //    with the basis column of n and hann[n] in registers; the 16 threads of a frame read its
-  //    spectrum together (broadcast reads)
+  };
+  issue(tile);
+
+  // B operands, the same for every tile: the irfft basis of this lane's k group with hann[n]
+  // folded in, and the synthesis taps (gain 4 folded in: an exact power-of-two scaling) of band
+  // lg for output n = 4q + r at each shift s
+  float ba[4], bf[19];
   {
-    const int n = n2;
-    constexpr int NFR = 4 * TAIL_NT, NG = TAIL_THREADS / 16;
+    const float h = hann[lm];
+    ba[0] = h * bc[lg * 16 + lm];
+    ba[1] = h * (lg == 0 ? bc[8 * 16 + lm] : bs[lg * 16 + lm]);
+    ba[2] = h * bc[(lg + 4) * 16 + lm];
+    ba[3] = h * bs[(lg + 4) * 16 + lm];
+    const int q = lm >> 2, r = lm & 3;
 #pragma unroll
-    for (int it = 0; it < (NFR + NG - 1) / NG; it++) {
-      const int f = g2 + it * NG;   // frame f of the block: band f / TAIL_NT, frame f % TAIL_NT
-      if (f < NFR) {
-        const int b = f / TAIL_NT, tt = f - b * TAIL_NT;
-        const float4 *re4 = reinterpret_cast<const float4 *>(s_re[b][tt]);
-        const float4 *im4 = reinterpret_cast<const float4 *>(s_im[b][tt]);
-        const float4 r0 = re4[0], r1 = re4[1], r2 = re4[2];
-        const float4 i0 = im4[0], i1 = im4[1], i2 = im4[2];
-        const float re[9] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w, r2.x};
-        const float im[9] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w, i2.x};
-        float fr = 0.0f, fi = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 9; k++) {
-          fr += re[k] * cb[k];
-          fi += im[k] * sb[k];
-        }
-        s_fr[b][tt][n] = (fr + fi) * hn;
-      }
+    for (int s = 0; s < 19; s++) {
+      const int j = s - q;
+      bf[s] = j >= 0 && j < 16 ? 4.0f * hp[(lg * 4 + r) * 16 + j] : 0.0f;
     }
   }
-  __syncthreads();
-  // 3) overlap-add, window-sum normalisation, [8:-8] trim (all bands' y over all threads)
-#pragma unroll
-  for (int it = 0; it < (4 * TAIL_NY + TAIL_THREADS - 1) / TAIL_THREADS; it++) {
-    const int e = tid + it * TAIL_THREADS;
-    if (e < 4 * TAIL_NY) {
-      const int b = e / TAIL_NY, ii = e - b * TAIL_NY;
-      const long long i = i_lo + ii;
-      float yv = 0.0f;
-      if (i >= 0 && i < Ly) {
-        const long long j = i + 8;
-        const int r = (int) (j & 3);
-        const long long qq = j >> 2;
-        float ola = 0.0f, ws = 0.0f;
-#pragma unroll
-        for (int jt = 0; jt < 4; jt++) {   // tap jt: frame t = qq - jt, sample n = r + 4*jt
-          const long long t = qq - jt;
-          if (t < 0 || t >= L) continue;
-          const int n = r + 4 * jt;
-          ola += s_fr[b][(int) (t - t_lo)][n];
-          ws += s_hann[n] * s_hann[n];
-        }
-        const float eps = 1e-9f;
-        yv = ola / (ws > eps ? ws : eps);
-      }
-      s_y[b][ii] = yv;
-    }
-  }
-  __syncthreads();
-  // 4) PQMF synthesis: zero-insert x4 (gain 4), 63-tap FIR per band, sum of bands.  Thread u
-  // makes samples o0 + 4u + r, r = 0..3: sample r uses the taps m = (3 - r) + 4j, and every one of
-  // the four reads the same y slots u + 1 + j (o0 is a multiple of 4), so the 16 y values of a band
-  // are read once for four samples, and the taps are the same for every thread (scalar loads).
-  // y outside [0, Ly) is stored as 0 above, so taps there add 0 and need no range test.
-  const int u = tid;
-  if (u >= TAIL_OUT / 4) return;
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int b = 0; b < 4; b++) {
-    float y[16];
-#pragma unroll
-    for (int j = 0; j < 16; j++) y[j] = 4.0f * s_y[b][u + 1 + j];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-#pragma unroll
-      for (int j = 0; j < 16; j++) {
-        if (3 - r + 4 * j < 63) acc[r] += hp[(b * 4 + r) * 16 + j] * y[j];
-      }
-    }
-  }
-  const long long ob = o0 + 4 * u;
   const float bias = hb[0];
+  // phase B: lane slot = lane + 64 it has jr & 3 = lane & 3, so its window-sum terms are fixed
+  float hh[4];
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const long long o = ob + r;
-    if (o < nout && o >= e_lo && o < e_hi) wav[o] = acc[r] + bias;
+  for (int jt = 0; jt < 4; jt++) {
+    const float h = hann[(lane & 3) + 4 * jt];
+    hh[jt] = h * h;
+  }
+  float *const pl = s_pl + w * 4 * P;        // this wave's band
+  float *const yw = s_y + w * YP + 3;
+
+  for (bool first = true;; first = false) {
+    const int item = tile / nbx;
+    const int o0 = (tile - item * nbx) * TOUT;
+    const int t_lo = o0 / 16 - 3;             // frame of relative index 0
+    const int i_lo = o0 / 4 - 8;              // y index of slot 0
+    // A) band w's frames, 16 per group: spectra into A, 4 MFMAs, the 16 x 16 result into the
+    //    overlap-add planes (row 4 lg + i of column lm is sample lm of frame 16c + 4lg + i)
+#pragma unroll
+    for (int c = 0; c < NG; c++) {
+      const int tf = t_lo + 16 * c + lm;
+      // the hardware transcendentals: v_exp_f32 is 2^x, v_sin_f32 / v_cos_f32 take revolutions
+      // (sin(2 pi x)).  The phase pi * sin(p) in revolutions is sin(p) / 2, within [-1/2, 1/2],
+      // so no range reduction is needed; p itself is a conv output of modest size.
+      const float m0 = __builtin_amdgcn_exp2f(ld[c][0] * 1.44269504f);
+      const float r0 = 0.5f * __builtin_amdgcn_sinf(ld[c][1] * 0.159154943f);
+      const float m1 = __builtin_amdgcn_exp2f(ld[c][2] * 1.44269504f);
+      const float r1 = 0.5f * __builtin_amdgcn_sinf(ld[c][3] * 0.159154943f);
+      const float m8 = __builtin_amdgcn_exp2f(ld[c][4] * 1.44269504f);
+      const float r8 = 0.5f * __builtin_amdgcn_sinf(ld[c][5] * 0.159154943f);
+      const bool ok = (unsigned) tf < (unsigned) L;   // frames outside the sequence are zero
+      const float a0 = ok ? m0 * __builtin_amdgcn_cosf(r0) : 0.0f;
+      const float a1 = ok ? (lg == 0 ? m8 * __builtin_amdgcn_cosf(r8) : m0 * __builtin_amdgcn_sinf(r0)) : 0.0f;
+      const float a2 = ok ? m1 * __builtin_amdgcn_cosf(r1) : 0.0f;
+      const float a3 = ok ? m1 * __builtin_amdgcn_sinf(r1) : 0.0f;
+      f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+      d = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, ba[0], d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, ba[1], d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x4f32(a2, ba[2], d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x4f32(a3, ba[3], d, 0, 0, 0);
+      float *const dst = pl + (lm >> 2) * P + 64 * c + 16 * lg + lm;
+#pragma unroll
+      for (int i = 0; i < 4; i++) dst[4 * i] = d[i];
+    }
+    const int next = next_kept(tile + (int) gridDim.x);
+    if (next < ntiles) issue(next);   // in flight through phases B and C
+    // the previous tile's phase C read every band's y
+    if (!first) __syncthreads();
+    // B) band w's y: overlap-add, window-sum normalisation, [8:-8] trim; 0 outside [0, Ly)
+#pragma unroll
+    for (int it = 0; it < (SLOTS + 63) / 64; it++) {
+      const int slot = lane + 64 * it;
+      if (slot < SLOTS) {
+        const int jr = slot + 12, i = i_lo + slot;
+        float yv = 0.0f;
+        if (i >= 0 && i < Ly) {
+          const float ola = ((pl[jr] + pl[P + jr]) + pl[2 * P + jr]) + pl[3 * P + jr];
+          const int t0 = t_lo + (jr >> 2);    // frame of tap jt is t0 - jt
+          float ws = 0.0f;
+#pragma unroll
+          for (int jt = 0; jt < 4; jt++) ws += (unsigned) (t0 - jt) < (unsigned) L ? hh[jt] : 0.0f;
+          const float eps = 1e-9f;
+          yv = ola / (ws > eps ? ws : eps);
+        }
+        yw[slot] = yv;
+      }
+    }
+    __syncthreads();
+    // C) PQMF synthesis of the 256-sample block w: A = y_lg[64w + 4m + 1 + s] (a lane's 20
+    //    consecutive values in five 16-byte reads), B = the taps of shift s; the result row
+    //    4lg + i, column lm is sample o0 + 256w + 16(4lg + i) + lm
+    if (w < NB) {
+      const float4 *ya = reinterpret_cast<const float4 *>(s_y + lg * YP + 64 * w + 4 * lm + 4);
+      float a[20];
+#pragma unroll
+      for (int v = 0; v < 5; v++) {
+        const float4 x = ya[v];
+        a[4 * v] = x.x; a[4 * v + 1] = x.y; a[4 * v + 2] = x.z; a[4 * v + 3] = x.w;
+      }
+      f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < 19; s++) d = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], bf[s], d, 0, 0, 0);
+      // samples outside the item or its kept range get an offset past the buffer: the store is
+      // dropped by the range check
+      const long long e_lo = item == 0 ? em.lo_first : em.lo;
+      const long long e_hi = item + 1 == batch ? em.hi_last : em.hi;
+      const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+          (void *) (wav + (long long) item * bsw), (short) 0, (int) 0x7fffffff, PTK_BUF_WORD3);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int o = o0 + 256 * w + 16 * (4 * lg + i) + lm;
+        const unsigned vo = o < nout && o >= e_lo && o < e_hi ? (unsigned) o * 4u : PTK_OOB;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(d[i] + bias), rw, vo, 0, 0);
+      }
+    }
+    if (next >= ntiles) break;
+    tile = next;
   }
 }
 
-template <int TOUT, int THR>
-static void launch_tail(unsigned blocks, int batch, const float *p, int64_t ldp, int64_t bsp,
-                        int64_t L, float *wav, int64_t bsw, const float *consts, ptk_emit em,
-                        hipStream_t s) {
-  hipLaunchKernelGGL((tail_kernel<TOUT, THR>), dim3(blocks, (unsigned) batch), dim3(THR), 0, s, p,
-                     (long long) ldp, (long long) bsp, (long long) L, wav, (long long) bsw, consts, em);
+template <int TOUT>
+static int launch_tail(int batch, const float *p, int64_t ldp, int64_t bsp, int64_t L, float *wav,
+                       int64_t bsw, const float *consts, ptk_emit em, int grid_knob, hipStream_t s) {
+  const int nout = (int) (16 * (L - 1));
+  const int nbx = (nout + TOUT - 1) / TOUT;
+  const long long ntiles = (long long) nbx * batch;
+  if (ntiles > INT_MAX / 2) {
+    set_err("ptk_tail: %lld tiles exceed the launch's index range", ntiles);
+    return -1;
+  }
+  // A workgroup per tile while the tiles fit on the chip at once; past that, as many workgroups
+  // as are resident, each looping over tiles with the next tile's reads in flight (PTK_TAIL_GRID:
+  // -1 = a workgroup per tile, n > 0 = n workgroups).
+  static const int resident = [] {
+    int ncu = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, tail_kernel<TOUT>, 256, 0) !=
+            hipSuccess)
+      return 0;
+    return ncu * per_cu;
+  }();
+  long long grid = grid_knob > 0 ? grid_knob : (grid_knob < 0 || resident <= 0 ? ntiles : resident);
+  if (grid > ntiles) grid = ntiles;
+  hipLaunchKernelGGL((tail_kernel<TOUT>), dim3((unsigned) grid), dim3(256), 0, s, p,
+                     (long long) ldp, (long long) bsp, (int) L, wav, (long long) bsw, consts, em,
+                     nbx, (int) ntiles);
+  HCHK(hipGetLastError());
+  return 0;
 }
 
 extern "C" int ptk_tail_batched(const float *p, int64_t ldp, int64_t bsp, int64_t L, float *wav,
@@ -1641,26 +1694,27 @@ extern "C" int ptk_tail_batched(const float *p, int64_t ldp, int64_t bsp, int64_
     set_err("ptk_tail: need at least 2 frames (got %lld)", (long long) L);
     return -1;
   }
+  // 32-bit buffer offsets: an item's 72 rows and its waveform within 2 GiB each
+  if (ldp < L || 72 * ldp * 4 > INT32_MAX || 16 * (L - 1) * 4 > INT32_MAX) {
+    set_err("ptk_tail: %lld frames (row stride %lld) past the kernel's 32-bit offsets",
+            (long long) L, (long long) ldp);
+    return -1;
+  }
   if (batch <= 0) return 0;
   const long long nout = 16 * (L - 1);
   const ptk_emit all = {0, 0, nout, nout};
   const ptk_emit em = emit ? *emit : all;
-  // Block size: 1024 samples (on 512 threads) once their grid gives every CU a block, else 512.
-  // Measured on MI355X, T = 226 requests: batch 1 5.6 us with 512 (6.9 with 1024: 57 blocks for
-  // 256 CUs), batch 8 9.3 us with 1024 (10.9 with 512), batch 64 45.6 us = 1.79 TB/s with 1024
-  // (61 us with 512): the larger block recomputes fewer halo frames (74 for 64 instead of 42 for
-  // 32) and runs fewer, longer-lived blocks through its three barriers.  PTK_TAIL_OUT=512 / 1024
-  // forces one.
-  const int knob = env_knob("PTK_TAIL_OUT");
-  const long long blocks1k = (nout + 1023) / 1024;
-  const bool big = knob == 1024 || (knob != 512 && blocks1k * batch >= 256);
+  // Tile size: PTK_TAIL_OUT=256 / 512 / 1024 forces one.
+  const int knob = env_knob("PTK_TAIL_OUT"), gknob = env_knob("PTK_TAIL_GRID");
+  const long long t1k = (nout + 1023) / 1024 * batch, t512 = (nout + 511) / 512 * batch;
   hipStream_t st = (hipStream_t) s;
-  if (big)
-    launch_tail<1024, 512>((unsigned) blocks1k, batch, p, ldp, bsp, L, wav, bsw, consts, em, st);
-  else
-    launch_tail<512, 512>((unsigned) ((nout + 511) / 512), batch, p, ldp, bsp, L, wav, bsw, consts, em, st);
-  HCHK(hipGetLastError());
-  return 0;
+  const int tout = knob == 256 || knob == 512 || knob == 1024
+      ? knob : (t1k >= 256 ? 1024 : (t512 >= 256 ? 512 : 256));
+  if (tout == 1024)
+    return launch_tail<1024>(batch, p, ldp, bsp, L, wav, bsw, consts, em, gknob, st);
+  if (tout == 512)
+    return launch_tail<512>(batch, p, ldp, bsp, L, wav, bsw, consts, em, gknob, st);
+  return launch_tail<256>(batch, p, ldp, bsp, L, wav, bsw, consts, em, gknob, st);
 }
 extern "C" int ptk_tail(const float *p, int64_t ldp, int64_t L, float *wav, const float *consts,
                         void *s) {

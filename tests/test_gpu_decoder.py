@@ -172,23 +172,28 @@ def test_tail_alone_vs_oracle(env, L, batch):
 
 @pytest.mark.parametrize("L,batch", [(2, 1), (65, 3), (3617, 2)])
 def test_tail_block_size_gives_the_same_samples(env, L, batch, monkeypatch):
-    """The tail kernel's block size (512 or 1024 samples, chosen from the grid; forced here through
-    PTK_TAIL_OUT) only changes which workgroup makes a sample: the waveform is bit-identical, and
-    within the oracle bar."""
+    """The tail kernel's tile size (256, 512 or 1024 samples, chosen from the work; forced here
+    through PTK_TAIL_OUT) and its grid (a workgroup per tile, or fewer workgroups looping over the
+    tiles: PTK_TAIL_GRID) only change which workgroup makes a sample: the waveform is
+    bit-identical, and within the oracle bar."""
     ctx, model, ws, bs = env
-    say(f"tail block sizes L={L} batch={batch}")
+    say(f"tail tile sizes and grids L={L} batch={batch}")
     rng = np.random.default_rng(7 * L + batch)
     p = (0.7 * rng.standard_normal((batch, 72, L))).astype(np.float32)
     dp = dev_of(ctx, p)
     dw = pkg.DevBuf(batch * 16 * (L - 1))
     outs = []
-    for size in ("512", "1024"):
+    for size, grid in (("256", "-1"), ("512", "-1"), ("1024", "-1"), ("256", "3"), ("1024", "2"),
+                       ("512", "0")):
         monkeypatch.setenv("PTK_TAIL_OUT", size)
+        monkeypatch.setenv("PTK_TAIL_GRID", grid)
         dw.upload(ctx, np.full(batch * 16 * (L - 1), np.nan, np.float32))
         assert ctx.lib.ptd_tail(ctx.ptr, model.ptr, dp.ptr, L, batch, dw.ptr) == 0
         outs.append(dw.download(ctx).reshape(batch, 16 * (L - 1)))
     monkeypatch.delenv("PTK_TAIL_OUT")
-    assert np.array_equal(outs[0], outs[1])
+    monkeypatch.delenv("PTK_TAIL_GRID")
+    for o in outs[1:]:
+        assert np.array_equal(outs[0], o)
     for i in range(batch):
         assert relerr(outs[1][i], ol.tail(p[i], ws[40], bs[40])) < 1e-4
     dp.free(); dw.free()
@@ -423,6 +428,32 @@ def test_window_columns_change_no_sample(env, T, win, cx, monkeypatch):
     wav = dw.download(ctx)
     assert np.all(np.isfinite(wav))
     assert np.array_equal(wav, whole)
+    dz.free(); dw.free()
+
+
+@pytest.mark.parametrize("tout,grid", [("256", "7"), ("1024", "3"), ("512", "-1")])
+def test_window_tail_tiles_and_grid_change_no_sample(env, tout, grid, monkeypatch):
+    """A windowed decode's tail skips the tiles with no kept samples: with a few workgroups looping
+    over the tiles (PTK_TAIL_GRID), or one per tile, at every tile size, the long-form request
+    (T = 1500 in 96/16 windows) is bit-identical to the default launch, and every sample is
+    written."""
+    ctx, model, ws, bs = env
+    say(f"windowed tail tiles {tout} grid {grid}")
+    lib = ctx.lib
+    T = 1500
+    z = synth.latent(T, 4242)
+    dz, dw = dev_of(ctx, z), pkg.DevBuf(256 * T)
+    assert lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, 96, 16, dw.ptr) == 0
+    ref = dw.download(ctx)
+    monkeypatch.setenv("PTK_TAIL_OUT", tout)
+    monkeypatch.setenv("PTK_TAIL_GRID", grid)
+    dw.upload(ctx, np.full(256 * T, np.nan, np.float32))
+    assert lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, 96, 16, dw.ptr) == 0
+    wav = dw.download(ctx)
+    monkeypatch.delenv("PTK_TAIL_OUT")
+    monkeypatch.delenv("PTK_TAIL_GRID")
+    assert np.all(np.isfinite(wav))
+    assert np.array_equal(wav, ref)
     dz.free(); dw.free()
 
 
