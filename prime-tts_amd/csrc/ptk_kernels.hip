@@ -1014,6 +1014,10 @@ static int env_knob(const char *name) {
   const char *e = getenv(name);
   return e ? atoi(e) : 0;
 }
+static int env_knob_or(const char *name, int dflt) {
+  const char *e = getenv(name);
+  return e ? atoi(e) : dflt;
+}
 
 // Tile shape (RB rows, channel split S in {1, 2, 4}; PTK_CONV_RB and PTK_CONV_SPLIT override).
 // All waves of a launch usually fit on the chip at once, so a launch lasts as long as its busiest
@@ -1480,11 +1484,25 @@ struct TailGeo {
   static constexpr int NB = TOUT / 256;      // 256-sample output blocks
 };
 
+// The launch's walk over the tiles.  Tiles are numbered item-major; workgroup b takes tiles
+// base, base + stride, ... below its end, passing over those with no kept sample.  With a
+// workgroup per tile: base = b, stride = the grid, end = all tiles.  When workgroups loop (the
+// grid a multiple of 8), the tiles are split into 8 contiguous runs, one per XCD (workgroup b runs
+// on XCD b % 8), and the XCD's workgroups take its run in order: neighbouring tiles, which read
+// the same boundary frames, then share that XCD's L2.  The stride steps (item, bx) by sq items
+// and sr tiles, so no division per step.  Each item's kept samples are [lo, hi) (clamped to its
+// samples; item 0 and the last item have their own bounds: the windows of a long request).
+struct TailWalk {
+  int nbx, batch, ntiles, xcd_run;   // xcd_run: tiles per XCD run, 0 = no split
+  int stride, sq, sr;
+  int lo_first, lo, hi, hi_last;
+};
+
 template <int TOUT>
 __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, long long ldp,
                                                    long long bsp, int L, float *__restrict__ wav,
                                                    long long bsw, const float *__restrict__ cst,
-                                                   ptk_emit em, int nbx, int ntiles) {
+                                                   TailWalk tw) {
   using G = TailGeo<TOUT>;
   constexpr int NG = G::NG, P = G::P, SLOTS = G::SLOTS, YP = G::YP, NB = G::NB;
   static_assert(NB >= 1 && NB <= 4 && TOUT % 256 == 0, "one 256-sample block per wave");
@@ -1495,22 +1513,29 @@ __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int lm = lane & 15, lg = lane >> 4;
   const float *hann = cst, *bc = cst + 16, *bs = cst + 160, *hp = cst + 304, *hb = cst + 560;
-  const int Ly = 4 * (L - 1), nout = 4 * Ly;
-  const int batch = ntiles / nbx;
+  const int Ly = 4 * (L - 1);
 
-  // the next tile at or after t (stepping by the grid) that holds samples of its item to keep
-  auto next_kept = [&](int t) {
-    for (; t < ntiles; t += (int) gridDim.x) {
-      const int item = t / nbx;
-      const long long o0 = (long long) (t - item * nbx) * TOUT;
-      const long long e_lo = item == 0 ? em.lo_first : em.lo;
-      const long long e_hi = item + 1 == batch ? em.hi_last : em.hi;
-      if (o0 < e_hi && o0 + TOUT > e_lo) break;
+  // this workgroup's tiles (TailWalk); (item, bx) = divmod(tile, nbx)
+  const int b0 = (int) blockIdx.x;
+  int tile = tw.xcd_run ? (b0 & 7) * tw.xcd_run + (b0 >> 3) : b0;
+  const int tend = tw.xcd_run ? min(((b0 & 7) + 1) * tw.xcd_run, tw.ntiles) : tw.ntiles;
+  int item = tile / tw.nbx, bx = tile - item * tw.nbx;
+  auto step = [&](int &t, int &it, int &b) {
+    t += tw.stride;
+    it += tw.sq;
+    b += tw.sr;
+    if (b >= tw.nbx) {
+      b -= tw.nbx;
+      it++;
     }
-    return t;
   };
-  int tile = next_kept((int) blockIdx.x);
-  if (tile >= ntiles) return;
+  auto kept_lo = [&](int it) { return it == 0 ? tw.lo_first : tw.lo; };
+  auto kept_hi = [&](int it) { return it + 1 == tw.batch ? tw.hi_last : tw.hi; };
+  auto to_kept = [&](int &t, int &it, int &b) {
+    while (t < tend && !(b * TOUT < kept_hi(it) && b * TOUT + TOUT > kept_lo(it))) step(t, it, b);
+  };
+  to_kept(tile, item, bx);
+  if (tile >= tend) return;
 
   // reads of one tile: for frame group c of band w, lane (m, g) reads frame t_lo + 16c + m of
   // bins g and g + 4 (magnitude and phase) and, in k group 0, bin 8.  The item's 72 rows are one
@@ -1519,11 +1544,10 @@ __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, 
   const unsigned nrec = (unsigned) (72 * ldp * 4), ldp4 = (unsigned) (ldp * 4);
   const unsigned ro = (unsigned) (18 * w + lg) * ldp4;
   float ld[NG][6];
-  auto issue = [&](int t) {
-    const int item = t / nbx;
-    const int t_lo = (t - item * nbx) * (TOUT / 16) - 3;
+  auto issue = [&](int it, int b) {
+    const int t_lo = b * (TOUT / 16) - 3;
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-        (void *) (p + (long long) item * bsp), (short) 0, (int) nrec, PTK_BUF_WORD3);
+        (void *) (p + (long long) it * bsp), (short) 0, (int) nrec, PTK_BUF_WORD3);
 #pragma unroll
     for (int c = 0; c < NG; c++) {
       const int tf = t_lo + 16 * c + lm;
@@ -1538,7 +1562,7 @@ __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, 
       ld[c][5] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, vo8, 9 * ldp4, 0));
     }
   };
-  issue(tile);
+  issue(item, bx);
 
   // B operands, the same for every tile: the irfft basis of this lane's k group with hann[n]
   // folded in, and the synthesis taps (gain 4 folded in: an exact power-of-two scaling) of band
@@ -1558,21 +1582,29 @@ __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, 
     }
   }
   const float bias = hb[0];
-  // phase B: lane slot = lane + 64 it has jr & 3 = lane & 3, so its window-sum terms are fixed
+  // phase B: lane slot = lane + 64 it has jr & 3 = lane & 3, so its window-sum terms hann^2 are
+  // fixed.  Every y is ola * (1 / max(wsum, 1e-9)), wsum summed over the valid terms in tap
+  // order: the interior value is computed once here, by the same operations.
+  const float eps = 1e-9f;
   float hh[4];
 #pragma unroll
   for (int jt = 0; jt < 4; jt++) {
     const float h = hann[(lane & 3) + 4 * jt];
     hh[jt] = h * h;
   }
+  float ws_in = 0.0f;
+#pragma unroll
+  for (int jt = 0; jt < 4; jt++) ws_in += hh[jt];
+  const float inv_in = 1.0f / (ws_in > eps ? ws_in : eps);
   float *const pl = s_pl + w * 4 * P;        // this wave's band
   float *const yw = s_y + w * YP + 3;
 
   for (bool first = true;; first = false) {
-    const int item = tile / nbx;
-    const int o0 = (tile - item * nbx) * TOUT;
+    const int o0 = bx * TOUT;
     const int t_lo = o0 / 16 - 3;             // frame of relative index 0
     const int i_lo = o0 / 4 - 8;              // y index of slot 0
+    // every frame and y slot of the tile inside the sequence: no range tests
+    const bool inner = t_lo >= 0 && t_lo + 16 * NG <= L && i_lo >= 0 && i_lo + SLOTS <= Ly;
     // A) band w's frames, 16 per group: spectra into A, 4 MFMAs, the 16 x 16 result into the
     //    overlap-add planes (row 4 lg + i of column lm is sample lm of frame 16c + 4lg + i)
 #pragma unroll
@@ -1587,11 +1619,16 @@ __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, 
       const float r1 = 0.5f * __builtin_amdgcn_sinf(ld[c][3] * 0.159154943f);
       const float m8 = __builtin_amdgcn_exp2f(ld[c][4] * 1.44269504f);
       const float r8 = 0.5f * __builtin_amdgcn_sinf(ld[c][5] * 0.159154943f);
-      const bool ok = (unsigned) tf < (unsigned) L;   // frames outside the sequence are zero
-      const float a0 = ok ? m0 * __builtin_amdgcn_cosf(r0) : 0.0f;
-      const float a1 = ok ? (lg == 0 ? m8 * __builtin_amdgcn_cosf(r8) : m0 * __builtin_amdgcn_sinf(r0)) : 0.0f;
-      const float a2 = ok ? m1 * __builtin_amdgcn_cosf(r1) : 0.0f;
-      const float a3 = ok ? m1 * __builtin_amdgcn_sinf(r1) : 0.0f;
+      float a0 = m0 * __builtin_amdgcn_cosf(r0);
+      float a1 = lg == 0 ? m8 * __builtin_amdgcn_cosf(r8) : m0 * __builtin_amdgcn_sinf(r0);
+      float a2 = m1 * __builtin_amdgcn_cosf(r1);
+      float a3 = m1 * __builtin_amdgcn_sinf(r1);
+      if (!inner && (unsigned) tf >= (unsigned) L) {   // frames outside the sequence are zero
+        a0 = 0.0f;
+        a1 = 0.0f;
+        a2 = 0.0f;
+        a3 = 0.0f;
+      }
       f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
       d = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, ba[0], d, 0, 0, 0);
       d = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, ba[1], d, 0, 0, 0);
@@ -1601,27 +1638,38 @@ __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, 
 #pragma unroll
       for (int i = 0; i < 4; i++) dst[4 * i] = d[i];
     }
-    const int next = next_kept(tile + (int) gridDim.x);
-    if (next < ntiles) issue(next);   // in flight through phases B and C
+    int ntile = tile, nitem = item, nxb = bx;
+    step(ntile, nitem, nxb);
+    to_kept(ntile, nitem, nxb);
+    const bool more = ntile < tend;
+    if (more) issue(nitem, nxb);   // in flight through phases B and C
     // the previous tile's phase C read every band's y
     if (!first) __syncthreads();
     // B) band w's y: overlap-add, window-sum normalisation, [8:-8] trim; 0 outside [0, Ly)
+    if (inner) {
 #pragma unroll
-    for (int it = 0; it < (SLOTS + 63) / 64; it++) {
-      const int slot = lane + 64 * it;
-      if (slot < SLOTS) {
-        const int jr = slot + 12, i = i_lo + slot;
-        float yv = 0.0f;
-        if (i >= 0 && i < Ly) {
-          const float ola = ((pl[jr] + pl[P + jr]) + pl[2 * P + jr]) + pl[3 * P + jr];
-          const int t0 = t_lo + (jr >> 2);    // frame of tap jt is t0 - jt
-          float ws = 0.0f;
+      for (int it = 0; it < (SLOTS + 63) / 64; it++) {
+        const int slot = lane + 64 * it, jr = slot + 12;
+        if (slot < SLOTS)
+          yw[slot] = (((pl[jr] + pl[P + jr]) + pl[2 * P + jr]) + pl[3 * P + jr]) * inv_in;
+      }
+    } else {
 #pragma unroll
-          for (int jt = 0; jt < 4; jt++) ws += (unsigned) (t0 - jt) < (unsigned) L ? hh[jt] : 0.0f;
-          const float eps = 1e-9f;
-          yv = ola / (ws > eps ? ws : eps);
+      for (int it = 0; it < (SLOTS + 63) / 64; it++) {
+        const int slot = lane + 64 * it;
+        if (slot < SLOTS) {
+          const int jr = slot + 12, i = i_lo + slot;
+          float yv = 0.0f;
+          if (i >= 0 && i < Ly) {
+            const float ola = ((pl[jr] + pl[P + jr]) + pl[2 * P + jr]) + pl[3 * P + jr];
+            const int t0 = t_lo + (jr >> 2);    // frame of tap jt is t0 - jt
+            float ws = 0.0f;
+#pragma unroll
+            for (int jt = 0; jt < 4; jt++) ws += (unsigned) (t0 - jt) < (unsigned) L ? hh[jt] : 0.0f;
+            yv = ola * (1.0f / (ws > eps ? ws : eps));
+          }
+          yw[slot] = yv;
         }
-        yw[slot] = yv;
       }
     }
     __syncthreads();
@@ -1639,27 +1687,30 @@ __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, 
       f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int s = 0; s < 19; s++) d = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], bf[s], d, 0, 0, 0);
-      // samples outside the item or its kept range get an offset past the buffer: the store is
-      // dropped by the range check
-      const long long e_lo = item == 0 ? em.lo_first : em.lo;
-      const long long e_hi = item + 1 == batch ? em.hi_last : em.hi;
+      // samples outside the item's kept range (which lies inside its samples) get an offset past
+      // the buffer: the store is dropped by the range check
+      const int lo = kept_lo(item), hi = kept_hi(item);
+      const unsigned cnt = hi > lo ? (unsigned) (hi - lo) : 0u;
       const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
           (void *) (wav + (long long) item * bsw), (short) 0, (int) 0x7fffffff, PTK_BUF_WORD3);
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int o = o0 + 256 * w + 16 * (4 * lg + i) + lm;
-        const unsigned vo = o < nout && o >= e_lo && o < e_hi ? (unsigned) o * 4u : PTK_OOB;
+        const unsigned vo = (unsigned) (o - lo) < cnt ? (unsigned) o * 4u : PTK_OOB;
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(d[i] + bias), rw, vo, 0, 0);
       }
     }
-    if (next >= ntiles) break;
-    tile = next;
+    if (!more) break;
+    tile = ntile;
+    item = nitem;
+    bx = nxb;
   }
 }
 
 template <int TOUT>
 static int launch_tail(int batch, const float *p, int64_t ldp, int64_t bsp, int64_t L, float *wav,
-                       int64_t bsw, const float *consts, ptk_emit em, int grid_knob, hipStream_t s) {
+                       int64_t bsw, const float *consts, const ptk_emit *em, int grid_knob,
+                       hipStream_t s) {
   const int nout = (int) (16 * (L - 1));
   const int nbx = (nout + TOUT - 1) / TOUT;
   const long long ntiles = (long long) nbx * batch;
@@ -1680,9 +1731,15 @@ static int launch_tail(int batch, const float *p, int64_t ldp, int64_t bsp, int6
   }();
   long long grid = grid_knob > 0 ? grid_knob : (grid_knob < 0 || resident <= 0 ? ntiles : resident);
   if (grid > ntiles) grid = ntiles;
+  // looping workgroups split the tiles into one contiguous run per XCD (PTK_TAIL_XCD=0: no split)
+  const int xcd_run = grid < ntiles && grid % 8 == 0 && env_knob_or("PTK_TAIL_XCD", 1)
+      ? (int) ((ntiles + 7) / 8) : 0;
+  const int stride = xcd_run ? (int) (grid / 8) : (int) grid;
+  auto clamp = [nout](int64_t v) { return (int) (v < 0 ? 0 : (v > nout ? nout : v)); };
+  const TailWalk tw = {nbx, batch, (int) ntiles, xcd_run, stride, stride / nbx, stride % nbx,
+                       clamp(em->lo_first), clamp(em->lo), clamp(em->hi), clamp(em->hi_last)};
   hipLaunchKernelGGL((tail_kernel<TOUT>), dim3((unsigned) grid), dim3(256), 0, s, p,
-                     (long long) ldp, (long long) bsp, (int) L, wav, (long long) bsw, consts, em,
-                     nbx, (int) ntiles);
+                     (long long) ldp, (long long) bsp, (int) L, wav, (long long) bsw, consts, tw);
   HCHK(hipGetLastError());
   return 0;
 }
@@ -1711,10 +1768,10 @@ extern "C" int ptk_tail_batched(const float *p, int64_t ldp, int64_t bsp, int64_
   const int tout = knob == 256 || knob == 512 || knob == 1024
       ? knob : (t1k >= 256 ? 1024 : (t512 >= 256 ? 512 : 256));
   if (tout == 1024)
-    return launch_tail<1024>(batch, p, ldp, bsp, L, wav, bsw, consts, em, gknob, st);
+    return launch_tail<1024>(batch, p, ldp, bsp, L, wav, bsw, consts, &em, gknob, st);
   if (tout == 512)
-    return launch_tail<512>(batch, p, ldp, bsp, L, wav, bsw, consts, em, gknob, st);
-  return launch_tail<256>(batch, p, ldp, bsp, L, wav, bsw, consts, em, gknob, st);
+    return launch_tail<512>(batch, p, ldp, bsp, L, wav, bsw, consts, &em, gknob, st);
+  return launch_tail<256>(batch, p, ldp, bsp, L, wav, bsw, consts, &em, gknob, st);
 }
 extern "C" int ptk_tail(const float *p, int64_t ldp, int64_t L, float *wav, const float *consts,
                         void *s) {

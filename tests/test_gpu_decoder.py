@@ -174,8 +174,8 @@ def test_tail_alone_vs_oracle(env, L, batch):
 def test_tail_block_size_gives_the_same_samples(env, L, batch, monkeypatch):
     """The tail kernel's tile size (256, 512 or 1024 samples, chosen from the work; forced here
     through PTK_TAIL_OUT) and its grid (a workgroup per tile, or fewer workgroups looping over the
-    tiles: PTK_TAIL_GRID) only change which workgroup makes a sample: the waveform is
-    bit-identical, and within the oracle bar."""
+    tiles, split into one run per XCD when the grid is a multiple of 8: PTK_TAIL_GRID) only change
+    which workgroup makes a sample: the waveform is bit-identical, and within the oracle bar."""
     ctx, model, ws, bs = env
     say(f"tail tile sizes and grids L={L} batch={batch}")
     rng = np.random.default_rng(7 * L + batch)
@@ -184,7 +184,7 @@ def test_tail_block_size_gives_the_same_samples(env, L, batch, monkeypatch):
     dw = pkg.DevBuf(batch * 16 * (L - 1))
     outs = []
     for size, grid in (("256", "-1"), ("512", "-1"), ("1024", "-1"), ("256", "3"), ("1024", "2"),
-                       ("512", "0")):
+                       ("512", "0"), ("256", "8"), ("512", "16")):
         monkeypatch.setenv("PTK_TAIL_OUT", size)
         monkeypatch.setenv("PTK_TAIL_GRID", grid)
         dw.upload(ctx, np.full(batch * 16 * (L - 1), np.nan, np.float32))
@@ -431,7 +431,8 @@ def test_window_columns_change_no_sample(env, T, win, cx, monkeypatch):
     dz.free(); dw.free()
 
 
-@pytest.mark.parametrize("tout,grid", [("256", "7"), ("1024", "3"), ("512", "-1")])
+@pytest.mark.parametrize("tout,grid", [("256", "7"), ("1024", "3"), ("512", "-1"), ("256", "8"),
+                                       ("1024", "24")])
 def test_window_tail_tiles_and_grid_change_no_sample(env, tout, grid, monkeypatch):
     """A windowed decode's tail skips the tiles with no kept samples: with a few workgroups looping
     over the tiles (PTK_TAIL_GRID), or one per tile, at every tile size, the long-form request
