@@ -260,90 +260,27 @@ def layer_table(csv_path, batch, counter_csv=None):
 
 
 def abi_leg(pkg, lib, ctx, model, ws, bs, T=226, reps=5):
-    """Config 4's request through the reference ABI with host buffers, the way the reference's
-    graph interpreter drives the library (pt_v21_host.c's conv / convT handlers): the decoder's 38
-    convs and 2 upsampling convTs as pt_v21_conv / pt_v21_convT calls on host arrays, weights and
-    biases resident in the process pool (wtab / btab), unpadded rows (conv_pad_in = pad), the
-    LeakyReLU after each c1 conv and after conv_pre fused as epilogue code 1, and the host ops
-    between the calls (LeakyReLU ahead of a conv, residual adds, branch averages, the reflect pad)
-    in numpy on the host.  Every call copies its input up and its output back and waits: this is
-    the PCIe-inclusive per-call path, reported beside the value, never as it.  conv_post's output
-    is compared with the device-resident decoder's (ptd_decode_stages) on the same latents."""
-    nrec = 40
-    pad_in0 = ctx.get_i64("conv_pad_in")
-    host = [np.ascontiguousarray(w, np.float32) for w in ws[:nrec]] + \
-           [np.ascontiguousarray(b, np.float32) for b in bs[:nrec]]
-    ptrs = (C.c_void_p * len(host))(*[h.ctypes.data for h in host])
-    sizes = (C.c_size_t * len(host))(*[h.nbytes for h in host])
-    if lib.ptd_pool_load(ctx.ptr, len(host), ptrs, sizes) != 0:
-        raise RuntimeError("ptd_pool_load failed")
-    calls = [0, 0]
-
-    def leaky(x, a):
-        return np.where(x >= 0, x, np.float32(a) * x).astype(np.float32)
-
-    def conv(x, i, cout, K, pad, dil, epi=0, a=0.0):
-        x = np.ascontiguousarray(x, np.float32)
-        cin, n_in = x.shape
-        n = n_in + 2 * pad - dil * (K - 1)
-        y = np.empty(((cout + 3) // 4 * 4, n), np.float32)
-        ctx.set_i64("conv_pad_in", pad)
-        if lib.pt_v21_conv(ctx.ptr, pkg.fptr(x), n_in, cin, pkg.fptr(y), n, n, cout, K, 1, pad,
-                           dil, pkg.fptr(host[i]), pkg.fptr(host[nrec + i]), 1, i, nrec + i, epi,
-                           0, a, 0.0) != 0:
-            raise RuntimeError(f"pt_v21_conv layer {i} failed")
-        calls[0] += 1
-        return y[:cout]
-
-    def convT(x, i, cout):
-        x = np.ascontiguousarray(x, np.float32)
-        cin, tin = x.shape
-        lout = (tin - 1) * 4 - 12 + 16
-        y = np.empty(((cout + 3) // 4 * 4, lout), np.float32)
-        if lib.pt_v21_convT(ctx.ptr, pkg.fptr(x), tin, cin, tin, pkg.fptr(y), lout, cout, 4, 6,
-                            16, pkg.fptr(host[i]), pkg.fptr(host[nrec + i]), 1, i, nrec + i) != 0:
-            raise RuntimeError(f"pt_v21_convT layer {i} failed")
-        calls[1] += 1
-        return y[:cout]
-
-    def mrf(x, base, C_, alpha):
-        l0 = leaky(x, 0.1)
-        outs = []
-        for br, K in enumerate((3, 7, 11)):
-            y = x
-            for j, d in enumerate((1, 3, 5)):
-                i1 = base + br * 6 + j * 2
-                a = conv(l0 if j == 0 else leaky(y, 0.1), i1, C_, K, d * (K - 1) // 2, d, 1, 0.1)
-                y = conv(a, i1 + 1, C_, K, (K - 1) // 2, 1) + y
-            outs.append(y)
-        return leaky((outs[0] + outs[1] + outs[2]) / np.float32(3.0), alpha)
-
-    def request(z):
-        h = conv(z, 0, 512, 7, 3, 1, 1, 0.1)
-        m0 = mrf(convT(h, 1, 256), 2, 256, 0.1)
-        m1 = mrf(convT(m0, 20, 128), 21, 128, 0.01)
-        return conv(np.concatenate([m1[:, 1:2], m1], axis=1), 39, 72, 7, 3, 1)
-
+    """Config 4's request through the reference ABI with host buffers (tests/abi_decoder.py: the
+    decoder's 38 convs and 2 upsampling convTs as pt_v21_conv / pt_v21_convT calls on host arrays,
+    driven the way the reference's interpreter drives the library).  Every call copies its input
+    up and its output back and waits: the PCIe-inclusive per-call path, reported beside the value,
+    never as it.  conv_post's output is compared with the device-resident decoder's
+    (ptd_decode_stages) on the same latents."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import abi_decoder
+    run = abi_decoder.AbiDecoder(pkg, ctx, ws, bs)
     z = pkg.synth.latent(T, 77)
-    p = request(z)
+    p = run.request(z)
     times = []
     for _ in range(reps):
         t0 = time.perf_counter()
-        request(z)
+        run.request(z)
         times.append(time.perf_counter() - t0)
     ms = float(np.median(times)) * 1e3
-    # the same latents through the device-resident decoder: conv_post's output
-    L = 16 * T + 1
-    dz, dw, dp = pkg.DevBuf.of(ctx, z), pkg.DevBuf(HOP * T), pkg.DevBuf(72 * L)
-    arr = (C.c_void_p * 6)(None, None, None, None, None, dp.ptr)
-    if lib.ptd_decode_stages(ctx.ptr, model.ptr, dz.ptr, T, dw.ptr, arr) != 0:
-        raise RuntimeError("ptd_decode_stages failed")
-    pd = dp.download(ctx).reshape(72, L)
-    for b in (dz, dw, dp):
-        b.free()
-    ctx.set_i64("conv_pad_in", pad_in0)
+    pd = abi_decoder.device_conv_post(pkg, ctx, model, z)
+    run.close()
     rel = float(np.max(np.abs(p.astype(np.float64) - pd)) / np.sqrt(np.mean(pd.astype(np.float64) ** 2)))
-    return {"frames": T, "conv_calls": calls[0] // (reps + 1), "convT_calls": calls[1] // (reps + 1),
+    return {"frames": T, "conv_calls": run.calls[0] // (reps + 1), "convT_calls": run.calls[1] // (reps + 1),
             "ms_per_request": round(ms, 3),
             "audio_s_per_s": round(T * HOP / SR / (ms * 1e-3), 2),
             "conv_post_vs_device_decoder_max_abs_over_rms": float(f"{rel:.3g}"),
