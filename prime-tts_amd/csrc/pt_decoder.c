@@ -748,6 +748,8 @@ static int win_schedule(int64_t T, int win_first, int win, int ctx, win_t *out, 
 }
 
 #define MAX_WIN 4096
+/* most streams a batched run of windows is split over */
+#define WIN_PARTS_MAX 4
 
 /* A schedule split into the launches that run it: the first window (alone when its width differs
  * from the others, or when asked to), then a run of full-width windows at a constant hop (one
@@ -799,6 +801,13 @@ static size_t win_plan_arena(const win_plan *pl, int win) {
   size_t b = 0, x;
   if (pl->first_alone && (x = ptd_decode_arena_bytes(pl->w0.w, 1)) > b) b = x;
   if (pl->nfull && (x = ptd_decode_arena_bytes(win, pl->nfull)) > b) b = x;
+  /* the batched run split over several streams holds every part's region at once */
+  for (int parts = 2; parts <= WIN_PARTS_MAX && pl->nfull >= parts; parts++) {
+    x = 0;
+    for (int p = 0; p < parts; p++)
+      x += al256(ptd_decode_arena_bytes(win, pl->nfull / parts + (p < pl->nfull % parts ? 1 : 0)));
+    if (x > b) b = x;
+  }
   if (pl->has_last && (x = ptd_decode_arena_bytes(pl->wl.w, 1)) > b) b = x;
   return b + 4096;
 }
@@ -810,15 +819,126 @@ static int win_one(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, con
   return decode_impl(c, m, z + l->a, T, 0, l->w, 1, wav + l->a * 256, 0, &em, NULL);
 }
 
-/* the batched run of full-width windows */
+/* windows [k0, k0 + nb) of the batched run of full-width windows, as one batched decode */
+static int win_range(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, const win_plan *pl,
+                     int k0, int nb, int win, int ctx, float *wav) {
+  const int64_t a = pl->wb0.a + (int64_t) (k0 - pl->b0) * pl->hop;
+  const int last = k0 + nb == pl->n;
+  const ptk_emit em = {k0 == 0 ? 0 : (int64_t) ctx * 256, (int64_t) ctx * 256,
+                       (int64_t) (win - ctx) * 256, (int64_t) (last ? win : win - ctx) * 256};
+  return decode_impl(c, m, z + a, T, pl->hop, win, nb, wav + a * 256, pl->hop * 256, &em, NULL);
+}
+
+/* ---- a context's extra streams
+ * A long batched run of windows is split in parts: the first on the context's stream, each other
+ * one on an extra stream of the context, made on first use and kept until the context shuts down
+ * (pt_ctx has the reference's layout, so the streams are held here, keyed by the context; a
+ * context is used by one thread at a time).  Each window's samples do not depend on the batch it
+ * runs in, and the parts write disjoint samples, so the output is the same.  The parts' launches
+ * overlap each other's ramp-up and tail, which a long request's batched launches leave idle when
+ * they run alone (in config 5, once the other requests are done). */
+#define AUX_MAX 256
+typedef struct {
+  pt_ctx *c;
+  void *s[WIN_PARTS_MAX - 1], *fork, *join[WIN_PARTS_MAX - 1];
+} aux_t;
+static pthread_mutex_t g_aux_lock = PTHREAD_MUTEX_INITIALIZER;
+static aux_t g_aux[AUX_MAX];
+
+static void aux_destroy(aux_t *a) {
+  for (int k = 0; k < WIN_PARTS_MAX - 1; k++) {
+    if (a->s[k]) {
+      ptk_stream_sync(a->s[k]);
+      ptk_stream_destroy(a->s[k]);
+    }
+    if (a->join[k]) ptk_event_destroy(a->join[k]);
+  }
+  if (a->fork) ptk_event_destroy(a->fork);
+  memset(a, 0, sizeof *a);
+}
+
+static aux_t *aux_get(pt_ctx *c) {
+  aux_t *r = NULL;
+  pthread_mutex_lock(&g_aux_lock);
+  for (int i = 0; i < AUX_MAX && !r; i++)
+    if (g_aux[i].c == c) r = &g_aux[i];
+  for (int i = 0; i < AUX_MAX && !r; i++) {
+    if (g_aux[i].c) continue;
+    aux_t a;
+    memset(&a, 0, sizeof a);
+    a.c = c;
+    int bad = ptk_event_create(&a.fork);
+    for (int k = 0; k < WIN_PARTS_MAX - 1 && !bad; k++)
+      bad = ptk_stream_create(&a.s[k]) || ptk_event_create(&a.join[k]);
+    if (bad) {
+      PT_LOG("extra streams of a context: %s", ptk_last_error());
+      aux_destroy(&a);
+    } else {
+      g_aux[i] = a;
+      r = &g_aux[i];
+    }
+    break;
+  }
+  pthread_mutex_unlock(&g_aux_lock);
+  return r;
+}
+
+void ptdi_aux_release(pt_ctx *c) {
+  pthread_mutex_lock(&g_aux_lock);
+  for (int i = 0; i < AUX_MAX; i++)
+    if (g_aux[i].c == c) aux_destroy(&g_aux[i]);
+  pthread_mutex_unlock(&g_aux_lock);
+}
+
+/* Parts of a batched run of n windows: a run of 16 or more in PTD_WINDOW_PARTS parts (default
+ * 2, at most 4, each at least 8 windows).  Measured on config 5 (the T = 1500 request's 22 full
+ * windows beside eight other requests): 2 parts +1.0 to +2.8 % against 1 (by box), 3 and 4 parts
+ * below 2.  PTD_WINDOW_STREAMS=1 never splits, =2 splits any run of two or more in two. */
+static int win_parts(int n) {
+  const char *e = getenv("PTD_WINDOW_STREAMS");
+  const int k = e ? atoi(e) : 0;
+  if (k == 1 || n < 2) return 1;
+  if (k == 2) return 2;
+  if (n < 16) return 1;
+  const char *pe = getenv("PTD_WINDOW_PARTS");
+  int p = pe ? atoi(pe) : 2;
+  if (p > WIN_PARTS_MAX) p = WIN_PARTS_MAX;
+  while (p > 2 && n / p < 8) p--;
+  return p < 1 ? 1 : p;
+}
+
+/* the batched run of full-width windows, on one stream or split over several */
 static int win_batch(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, const win_plan *pl,
                      int win, int ctx, float *wav) {
-  const int last_full = pl->b0 + pl->nfull == pl->n;
-  const ptk_emit em = {pl->b0 == 0 ? 0 : (int64_t) ctx * 256, (int64_t) ctx * 256,
-                       (int64_t) (win - ctx) * 256,
-                       (int64_t) (last_full ? win : win - ctx) * 256};
-  return decode_impl(c, m, z + pl->wb0.a, T, pl->hop, win, pl->nfull, wav + pl->wb0.a * 256,
-                     pl->hop * 256, &em, NULL);
+  const int parts = win_parts(pl->nfull);
+  aux_t *x = parts > 1 ? aux_get(c) : NULL;
+  if (!x) return win_range(c, m, z, T, pl, pl->b0, pl->nfull, win, ctx, wav);
+  /* the extra streams start after everything queued on the context's stream so far */
+  if (ptk_event_record(x->fork, c->g_stream)) return -1;
+  for (int k = 0; k < parts - 1; k++)
+    if (ptk_stream_wait_event(x->s[k], x->fork)) return -1;
+  void *s0 = c->g_stream;
+  const size_t used0 = c->g_arena_used;
+  size_t used = used0;
+  int rc = 0, k0 = pl->b0, started = 0;
+  for (int p = 0; p < parts && rc == 0; p++) {
+    const int nb = pl->nfull / parts + (p < pl->nfull % parts ? 1 : 0);
+    /* each part's activations after the previous parts' regions, which their kernels still use */
+    c->g_arena_used = used;
+    c->g_stream = p == 0 ? s0 : x->s[p - 1];
+    rc = win_range(c, m, z, T, pl, k0, nb, win, ctx, wav);
+    started = p + 1;
+    used = al256(used) + al256(ptd_decode_arena_bytes(win, nb));
+    k0 += nb;
+  }
+  c->g_stream = s0;
+  c->g_arena_used = used0;
+  /* whatever is queued on the context next (and reuses its arena) waits for every part */
+  for (int p = 1; p < started; p++)
+    if (ptk_event_record(x->join[p - 1], x->s[p - 1]) ||
+        ptk_stream_wait_event(c->g_stream, x->join[p - 1]))
+      rc = -1;
+  return rc;
 }
 
 size_t ptd_windows2_arena_bytes(int64_t T, int win_first, int win, int ctx) {

@@ -64,6 +64,8 @@ double ptdi_now_ms(void);
 
 /* windowed decode with the reference's first / later widths; t_first != NULL: window 0 is
  * decoded alone, waited for, and its completion time stored there */
+/* releases the second stream a context's windowed decodes may have made (pt_decoder.c) */
+void ptdi_aux_release(pt_ctx *c);
 int ptdi_decode_windows(pt_ctx *c, const struct ptd_model *m, const float *z, int64_t T,
                         int win_first, int win, int ctx, float *wav, double *t_first);
 

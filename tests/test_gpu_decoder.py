@@ -458,6 +458,41 @@ def test_window_tail_tiles_and_grid_change_no_sample(env, tout, grid, monkeypatc
     dz.free(); dw.free()
 
 
+@pytest.mark.parametrize("T,mode", [(1500, "default"), (300, "2"), (1500, "2"), (600, "default")])
+def test_window_streams_change_no_sample(env, T, mode, monkeypatch):
+    """A batched run of windows split over the context's stream and a second stream (the default
+    for runs of 16 windows or more; PTD_WINDOW_STREAMS=2 splits any run of two, =1 none) gives the
+    same samples as the unsplit run, bit for bit, with the context's arena poisoned first; and a
+    decode queued on the context right after it, which reuses the arena the second half used,
+    still matches its own reference (it waits for the second stream)."""
+    ctx, model, ws, bs = env
+    say(f"window streams T={T} mode={mode}")
+    lib = ctx.lib
+    z = synth.latent(T, 7100 + T)
+    z2 = synth.latent(150, 7200)
+    dz, dw = dev_of(ctx, z), pkg.DevBuf(256 * T)
+    dz2, dw2 = dev_of(ctx, z2), pkg.DevBuf(256 * 150)
+    monkeypatch.setenv("PTD_WINDOW_STREAMS", "1")
+    assert lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, 96, 16, dw.ptr) == 0
+    ref = dw.download(ctx)
+    assert lib.ptd_decode(ctx.ptr, model.ptr, dz2.ptr, 150, 1, dw2.ptr) == 0
+    ref2 = dw2.download(ctx)
+    if mode == "default":
+        monkeypatch.delenv("PTD_WINDOW_STREAMS")
+    else:
+        monkeypatch.setenv("PTD_WINDOW_STREAMS", mode)
+    for rep in range(2):
+        dw.upload(ctx, np.full(256 * T, np.nan, np.float32))
+        dw2.upload(ctx, np.full(256 * 150, np.nan, np.float32))
+        assert lib.ptd_debug_fill_arena(ctx.ptr, 0xFF) == 0
+        assert lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, 96, 16, dw.ptr) == 0
+        assert lib.ptd_decode(ctx.ptr, model.ptr, dz2.ptr, 150, 1, dw2.ptr) == 0
+        assert np.array_equal(dw.download(ctx), ref), f"rep {rep}"
+        assert np.array_equal(dw2.download(ctx), ref2), f"rep {rep}"
+    for b in (dz, dw, dz2, dw2):
+        b.free()
+
+
 @pytest.mark.parametrize("T,win,cx", [(20, 32, 8), (57, 32, 8), (70, 32, 8), (300, 96, 16), (50, 16, 0)])
 def test_stream_chunks_stitched_equal_windows(env, T, win, cx):
     """ptd_decode_chunk window by window, stitched the way the reference's --stream driver does
