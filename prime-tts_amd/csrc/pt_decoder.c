@@ -910,7 +910,16 @@ static int win_parts(int n) {
 /* the batched run of full-width windows, on one stream or split over several */
 static int win_batch(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, const win_plan *pl,
                      int win, int ctx, float *wav) {
-  const int parts = win_parts(pl->nfull);
+  int parts = win_parts(pl->nfull);
+  /* every part's region must fit in the arena at once; else the run stays on one stream */
+  if (parts > 1) {
+    size_t need = 0;
+    for (int p = 0; p < parts; p++)
+      need += al256(ptd_decode_arena_bytes(win, pl->nfull / parts + (p < pl->nfull % parts ? 1 : 0)));
+    const size_t free_b = c->g_arena_bytes > al256(c->g_arena_used)
+        ? c->g_arena_bytes - al256(c->g_arena_used) : 0;
+    if (need > free_b) parts = 1;
+  }
   aux_t *x = parts > 1 ? aux_get(c) : NULL;
   if (!x) return win_range(c, m, z, T, pl, pl->b0, pl->nfull, win, ctx, wav);
   /* the extra streams start after everything queued on the context's stream so far */

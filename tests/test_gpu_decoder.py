@@ -493,6 +493,33 @@ def test_window_streams_change_no_sample(env, T, mode, monkeypatch):
         b.free()
 
 
+def test_window_split_falls_back_to_one_stream_in_a_small_arena(env, monkeypatch):
+    """A context whose arena holds the unsplit batched run (22 windows of the T = 1500 request) but
+    not both halves of the split at once keeps the run on its own stream: the decode succeeds and
+    matches the split decode of a roomy context bit for bit."""
+    ctx, model, ws, bs = env
+    say("window split fallback in a small arena")
+    lib = ctx.lib
+    T = 1500
+    z = synth.latent(T, 7300)
+    dz, dref, dw = dev_of(ctx, z), pkg.DevBuf(256 * T), pkg.DevBuf(256 * T)
+    assert lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, 96, 16, dref.ptr) == 0
+    ref = dref.download(ctx)
+    unsplit = int(lib.ptd_decode_arena_bytes(96, 22))
+    assert int(lib.ptd_windows_arena_bytes(T, 96, 16)) > unsplit + 2048
+    srv = lib.ptd_server_create(1, unsplit + 2048)
+    assert srv
+    try:
+        c = lib.ptd_server_ctx(srv, 0)
+        assert lib.ptd_decode_windows(c, model.ptr, dz.ptr, T, 96, 16, dw.ptr) == 0
+        assert lib.ptd_device_sync() == 0
+    finally:
+        lib.ptd_server_destroy(srv)
+    assert np.array_equal(dw.download(ctx), ref)
+    for b in (dz, dref, dw):
+        b.free()
+
+
 @pytest.mark.parametrize("T,win,cx", [(20, 32, 8), (57, 32, 8), (70, 32, 8), (300, 96, 16), (50, 16, 0)])
 def test_stream_chunks_stitched_equal_windows(env, T, win, cx):
     """ptd_decode_chunk window by window, stitched the way the reference's --stream driver does
