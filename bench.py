@@ -6,11 +6,12 @@ One step = BASELINE config 5, the largest single-GPU configuration: 8 independen
 long-form request of T = 1500 frames through 96-frame overlap-save windows with 16-frame context
 on a ninth context, all sharing one uploaded weight set.  Inputs are resident in HBM before the
 timed region; `value` is the step's audio seconds divided by its wall time.  Alongside: config 4
-(one request, T = 226) on one stream, eager, replayed as a HIP graph and eight at a time, the
-long-form request window by window (time to first audio) and batched, the container load and
-pt_v21_matmul, configs 1-3 in TFLOP/s, the dominant kernel against the
-fp32-MFMA roofline (HIP events on the stream it runs on), and the reference's CPU conv path timed
-on this host on a bounded sample.
+(one request, T = 226) on one stream, eager, replayed as a HIP graph and eight at a time, and
+driven through the reference ABI on host buffers (PCIe-inclusive); the long-form request window by
+window (time to first audio) and batched; the queue-fed server; the container load and
+pt_v21_matmul; configs 1-3 in TFLOP/s; the dominant kernel against the fp32-MFMA roofline and the
+tail kernel against HBM (HIP events on the stream they run on); and the reference's CPU conv path
+timed on this host on a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
        python bench.py --kernel-loop N   (only the dominant kernel and the tail kernel, N launches
