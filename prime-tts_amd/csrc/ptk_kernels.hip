@@ -490,14 +490,14 @@ template <int NB> struct WinGeo {
 //
 // LDS of one workgroup: per wave its staging area, and the partial-sum area (the staging area
 // itself when the partial sums fit in it).
-template <int NB, int RB> struct LdsGeo {
+template <int NB, int RB, int NW> struct LdsGeo {
   static constexpr int XWMAX = WinGeo<NB>::XWMAX;
   static constexpr int PS = RB == 32 ? XWMAX : XWMAX + 16;   // plane stride (float4 / float2)
   static constexpr int STG = 8 * PS;                         // staging floats per wave
   static constexpr int NV = RB / 2;                          // accumulators per lane and column block
   static constexpr int RED = NB * NV * 64;                   // partial-sum floats per wave
   static constexpr bool OWN_RED = RED <= STG;
-  static constexpr size_t BYTES = (size_t) CONV_WAVES * (STG > RED ? STG : RED) * sizeof(float);
+  static constexpr size_t BYTES = (size_t) NW * (STG > RED ? STG : RED) * sizeof(float);
 };
 
 // word 3 of a raw buffer resource on gfx9-family parts (gfx950): 32-bit data, range checked
@@ -518,19 +518,20 @@ __device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, unsigned vof
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
 
-// One workgroup = 4 waves.  The waves form 4/S column groups of S waves; the S waves of a group
-// compute the same RB-row x 32*NB-column output block over disjoint quarters/halves of the input
-// channels (S = 1: each wave its own block over all channels) and are reduced through LDS in wave
-// order (deterministic).  KT > 0: every problem of the group has K <= KT and the whole next chunk's
+// One workgroup = NW waves (4, or 8 for the 8-way split).  The waves form NW/S column groups of S
+// waves; the S waves of a group compute the same RB-row x 32*NB-column output block over disjoint
+// eighths/quarters/halves of the input channels (S = 1: each wave its own block over all channels)
+// and are reduced through LDS in wave order (deterministic).  NW = 8 runs S = 8 only.  KT > 0: every problem of the group has K <= KT and the whole next chunk's
 // A operands (KT float4 / float2 per lane) are prefetched while the current chunk runs; KT == 0:
 // any K, A loaded per tap.  IN: input transform (PTK_IN_*).  RB: rows per tile, 32 (32x32x2 MFMA,
 // weights from d.w) or 16 (16x16x4 MFMA on two 16-column blocks, weights from d.w16).
-template <int KT, int NB, int IN, int RB>
-__global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
+template <int KT, int NB, int IN, int RB, int NW>
+__global__ void __launch_bounds__(64 * NW) conv_mfma_kernel(const ConvGroup g) {
   extern __shared__ float smem[];
   static_assert(RB == 32 || (RB == 16 && NB == 1), "16-row tiles are built for one column block");
+  static_assert(NW == 4 || (NW == 8 && NB == 1), "8-wave workgroups are built for one column block");
   constexpr int NJ = WinGeo<NB>::NJ, XWMAX = WinGeo<NB>::XWMAX;
-  using Geo = LdsGeo<NB, RB>;
+  using Geo = LdsGeo<NB, RB, NW>;
   constexpr int PS = Geo::PS, NV = Geo::NV;
   // Grid row blockIdx.y is the problem, so every field of it can be fetched at entry; rows are
   // as long as the largest problem's workgroup count, and the excess of a shorter one exits.
@@ -553,7 +554,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   const int mb = r - tn * mt;
   const bool last_item = b == pi.nitem - 1;
   const long long q0i = d.q0 - (long long) (pi.ext_l & ~past0);   // this item's first column
-  const int S = g.split, lgS = g.lg_split, G = 4 >> lgS;
+  const int S = g.split, lgS = g.lg_split, G = NW >> lgS;
 
   // descriptor fields used in loops, read once (the problem index is dynamic, so the compiler
   // would otherwise re-read them from the kernel arguments)
@@ -839,7 +840,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   auto reduced = [&](int nb, int v) {
     float sum = red_of(wg0)[(nb * NV + v) * 64 + lane];
 #pragma unroll
-    for (int i = 1; i < 4; i++)
+    for (int i = 1; i < NW; i++)
       if (i < S) sum += red_of(wg0 + i)[(nb * NV + v) * 64 + lane];
     return sum;
   };
@@ -853,9 +854,10 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
   // them, one branch per op.
   if ((pi.flags & PROB_FAST) && one_phase && mb * RB + RB <= pi.M) {
     const ConvEpi ep = g.ep[p];
-    constexpr int NMAX = RB == 32 ? 16 : 8;
-    // values come in groups of GRP that a wave finishes together (nv is a multiple of GRP)
-    constexpr int GRP = RB == 32 ? 4 : 2, NG = NMAX / GRP;
+    // a wave finishes at most NMAX values (NV over the smallest split of its workgroup size),
+    // in groups of GRP that share a column block (nv is a multiple of GRP)
+    constexpr int NMAX = NW == 8 ? NV / 8 : NV;
+    constexpr int GRP = (RB == 32 ? 4 : 2) < NMAX ? (RB == 32 ? 4 : 2) : NMAX, NG = NMAX / GRP;
     const int ngrp = nv / GRP;
     const long long row0 = (long long) mb * RB - (long long) r_tile * ep.C4;   // first channel
     const int ldy32 = ep.ldy, ldt32 = ep.ldt;
@@ -885,6 +887,10 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
         cl[cb] = ok[cb] ? col : 0;
       }
       auto cbo = [&](int i) { return RB == 32 ? 0 : ((v0 + i) >> 2); };
+      // column / test of column block c as a select (an index into cl / ok that is not a
+      // compile-time constant would put the arrays in scratch memory)
+      auto clof = [&](int c) { return NCB == 1 || c == 0 ? cl[0] : cl[NCB - 1]; };
+      auto okof = [&](int c) { return NCB == 1 || c == 0 ? ok[0] : ok[NCB - 1]; };
       float rv[NMAX], val[NMAX];
       if (addt >= 0) {
 #pragma unroll
@@ -893,7 +899,7 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
 #pragma unroll
             for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++)
             rv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                rt, (unsigned) (lrow * ldt32 + cl[cbo(i)]) * 4u, (unsigned) (urow(i) * ldt32) * 4u, 0));
+                rt, (unsigned) (lrow * ldt32 + clof(cbo(i))) * 4u, (unsigned) (urow(i) * ldt32) * 4u, 0));
       }
 #pragma unroll
       for (int gg = 0; gg < NG; gg++)
@@ -954,15 +960,15 @@ __global__ void __launch_bounds__(256) conv_mfma_kernel(const ConvGroup g) {
               if (gg < ngrp)
 #pragma unroll
                 for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++)
-                val[i] = val[i] + ee.t[(long long) b * ee.bst + (row0 + lrow + urow(i)) * ee.ldt + cl[cbo(i)]];
+                val[i] = val[i] + ee.t[(long long) b * ee.bst + (row0 + lrow + urow(i)) * ee.ldt + clof(cbo(i))];
           }
         }
       }
       // a group shares its column block, so one test covers its stores
 #pragma unroll
       for (int gg = 0; gg < NG; gg++)
-        if (gg < ngrp && ok[cbo(gg * GRP)]) {
-          const unsigned vo = (unsigned) (lrow * ldy32 + cl[cbo(gg * GRP)]) * 4u;
+        if (gg < ngrp && okof(cbo(gg * GRP))) {
+          const unsigned vo = (unsigned) (lrow * ldy32 + clof(cbo(gg * GRP))) * 4u;
 #pragma unroll
           for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++) {
             const unsigned so = (unsigned) (urow(i) * ldy32) * 4u;
@@ -1019,7 +1025,7 @@ static int env_knob_or(const char *name, int dflt) {
   return e ? atoi(e) : dflt;
 }
 
-// Tile shape (RB rows, channel split S in {1, 2, 4}; PTK_CONV_RB and PTK_CONV_SPLIT override).
+// Tile shape (RB rows, channel split S in {1, 2, 4, 8}; PTK_CONV_RB and PTK_CONV_SPLIT override).
 // All waves of a launch usually fit on the chip at once, so a launch lasts as long as its busiest
 // SIMD: with W waves over the 1024 SIMDs (256 CUs x 4) that SIMD holds ceil(W / 1024) of them
 // while the mean is W / 1024.  Fewer than ~3 waves per SIMD also leave MFMA latency exposed (a
@@ -1057,6 +1063,7 @@ static int choose_tiles(const ptk_conv_desc *const *ds, int n, int nb, int *rb_o
   for (int i = 0; i < n; i++)
     if (ds[i]->w16 == nullptr) rb16_ok = false;
   int best = 4, best_rb = 32;
+  long long best_waves = 0;
   double best_eff = -1.0;
   for (int RB = 32; RB >= 16; RB /= 2) {
     if (RB == 16 && !rb16_ok) continue;
@@ -1082,9 +1089,20 @@ static int choose_tiles(const ptk_conv_desc *const *ds, int n, int nb, int *rb_o
         best_eff = e;
         best = S;
         best_rb = RB;
+        best_waves = waves;
       }
     }
   }
+  // The 8-way split (8-wave workgroups over the same tiles): for a single problem whose 4-way
+  // grid leaves one lone wave on most SIMDs (1 to 1.5 waves per SIMD), it doubles the waves that
+  // hide each other's latency at the cost of twice the partial sums.  Needs whole chunks for all
+  // eight waves (cinp a multiple of 64).  PTK_CONV_SPLIT=8 forces it where it applies,
+  // PTK_CONV_S8=0 turns the rule off, PTK_CONV_S8_MAX sets the upper bound in waves (1536).
+  const bool s8_ok = nb == 1 && n == 1 && ds[0]->cinp % (8 * CONV_CK) == 0;
+  const long long s8_max = env_knob_or("PTK_CONV_S8_MAX", 1536);
+  if (s8_ok && (env_s == 8 || (env_s == 0 && env_knob_or("PTK_CONV_S8", 1) != 0 && best == 4 &&
+                               best_waves >= (long long) kSimds && best_waves < s8_max)))
+    best = 8;
   *rb_out = best_rb;
   return best;
 }
@@ -1107,25 +1125,25 @@ extern "C" int ptk_conv_mfma_ok(const ptk_conv_desc *d) {
   return 1;
 }
 
-template <int KT, int NB, int IN, int RB>
+template <int KT, int NB, int IN, int RB, int NW>
 static void launch_conv(const ConvGroup &g, dim3 grid, hipStream_t s) {
-  constexpr size_t lds = LdsGeo<NB, RB>::BYTES;
-  hipLaunchKernelGGL((conv_mfma_kernel<KT, NB, IN, RB>), grid, dim3(256), lds, s, g);
+  constexpr size_t lds = LdsGeo<NB, RB, NW>::BYTES;
+  hipLaunchKernelGGL((conv_mfma_kernel<KT, NB, IN, RB, NW>), grid, dim3(64 * NW), lds, s, g);
 }
 
-template <int NB, int IN, int RB>
+template <int NB, int IN, int RB, int NW>
 static void launch_conv_k(int kmax, const ConvGroup &g, dim3 grid, hipStream_t s) {
-  if (kmax <= 3) launch_conv<3, NB, IN, RB>(g, grid, s);
-  else if (kmax == 4) launch_conv<4, NB, IN, RB>(g, grid, s);
-  else if (kmax <= 7) launch_conv<7, NB, IN, RB>(g, grid, s);
-  else if (kmax <= 11) launch_conv<11, NB, IN, RB>(g, grid, s);
-  else launch_conv<0, NB, IN, RB>(g, grid, s);
+  if (kmax <= 3) launch_conv<3, NB, IN, RB, NW>(g, grid, s);
+  else if (kmax == 4) launch_conv<4, NB, IN, RB, NW>(g, grid, s);
+  else if (kmax <= 7) launch_conv<7, NB, IN, RB, NW>(g, grid, s);
+  else if (kmax <= 11) launch_conv<11, NB, IN, RB, NW>(g, grid, s);
+  else launch_conv<0, NB, IN, RB, NW>(g, grid, s);
 }
 
-template <int NB, int RB>
+template <int NB, int RB, int NW>
 static void launch_conv_in(int in_op, int kmax, const ConvGroup &g, dim3 grid, hipStream_t s) {
-  if (in_op == PTK_IN_LEAKY) launch_conv_k<NB, PTK_IN_LEAKY, RB>(kmax, g, grid, s);
-  else launch_conv_k<NB, PTK_IN_PLAIN, RB>(kmax, g, grid, s);
+  if (in_op == PTK_IN_LEAKY) launch_conv_k<NB, PTK_IN_LEAKY, RB, NW>(kmax, g, grid, s);
+  else launch_conv_k<NB, PTK_IN_PLAIN, RB, NW>(kmax, g, grid, s);
 }
 
 extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream) {
@@ -1185,9 +1203,9 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
   }
   if (g.ngroup == 0) return 0;
   int rb = 32, maxcount = 0;
-  const int S = choose_tiles(live, g.ngroup, nb, &rb), G = 4 / S;
+  const int S = choose_tiles(live, g.ngroup, nb, &rb), NW = S == 8 ? 8 : 4, G = NW / S;
   g.split = S;
-  g.lg_split = S == 4 ? 2 : S == 2 ? 1 : 0;
+  g.lg_split = S == 8 ? 3 : S == 4 ? 2 : S == 2 ? 1 : 0;
   for (int i = 0; i < g.ngroup; i++) {
     const ptk_conv_desc *d = live[i];
     ConvProb &pi = g.info[i];
@@ -1257,9 +1275,11 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
   if (total == 0) return 0;
   hipStream_t s = (hipStream_t) stream;
   const dim3 grid((unsigned) maxcount, (unsigned) g.ngroup);
-  if (nb == 2) launch_conv_in<2, 32>(in_op, kmax, g, grid, s);
-  else if (rb == 16) launch_conv_in<1, 16>(in_op, kmax, g, grid, s);
-  else launch_conv_in<1, 32>(in_op, kmax, g, grid, s);
+  if (nb == 2) launch_conv_in<2, 32, 4>(in_op, kmax, g, grid, s);
+  else if (NW == 8 && rb == 16) launch_conv_in<1, 16, 8>(in_op, kmax, g, grid, s);
+  else if (NW == 8) launch_conv_in<1, 32, 8>(in_op, kmax, g, grid, s);
+  else if (rb == 16) launch_conv_in<1, 16, 4>(in_op, kmax, g, grid, s);
+  else launch_conv_in<1, 32, 4>(in_op, kmax, g, grid, s);
   HCHK(hipGetLastError());
   return 0;
 }

@@ -240,7 +240,7 @@ LAYER_COLS = [(0, 150, 20, 70, 13, 31), (1, 60, 9, 33, 5, 17), (20, 90, 30, 41, 
               (39, 257, 64, 128, 40, 65)]
 
 
-@pytest.mark.parametrize("rb,split", [(0, 0), (16, 1), (32, 2), (32, 4), (16, 4)])
+@pytest.mark.parametrize("rb,split", [(0, 0), (16, 1), (32, 2), (32, 4), (16, 4), (16, 8), (32, 8)])
 def test_layer_cols_per_item(env, rb, split, monkeypatch):
     """A launch over part of the columns (the windowed decode's form: middle items [q0, q0 + nq),
     item 0 from ext_l earlier, the last item to ext_r later, tile shape of the full width) writes
@@ -283,10 +283,12 @@ def test_layer_cols_per_item(env, rb, split, monkeypatch):
             dx.free(); dfull.free(); dy.free()
 
 
-@pytest.mark.parametrize("rb,split", [(16, 1), (16, 2), (16, 4), (32, 1), (32, 2), (32, 4)])
+@pytest.mark.parametrize("rb,split", [(16, 1), (16, 2), (16, 4), (16, 8), (32, 1), (32, 2), (32, 4),
+                                      (32, 8)])
 def test_tile_shapes_vs_oracle(env, rb, split, monkeypatch):
-    """Every tile shape the launcher can pick (16- or 32-row tiles, channel split 1 / 2 / 4; forced
-    through PTK_CONV_RB / PTK_CONV_SPLIT) against the oracle: a conv with a LeakyReLU epilogue,
+    """Every tile shape the launcher can pick (16- or 32-row tiles, channel split 1 / 2 / 4, and 8
+    on the single-problem launches; forced through PTK_CONV_RB / PTK_CONV_SPLIT) against the
+    oracle: a conv with a LeakyReLU epilogue,
     both convT phase forms (input LeakyReLU, C4 = 256 and 128), the 72-row conv_post whose last
     row block is partial, an MRF stack (grouped K 3 / 7 / 11, residual adds, branch sums) and a
     whole decode."""
