@@ -1093,15 +1093,18 @@ static int choose_tiles(const ptk_conv_desc *const *ds, int n, int nb, int *rb_o
       }
     }
   }
-  // The 8-way split (8-wave workgroups over the same tiles): for a single problem whose 4-way
-  // grid leaves one lone wave on most SIMDs (1 to 1.5 waves per SIMD), it doubles the waves that
-  // hide each other's latency at the cost of twice the partial sums.  Needs whole chunks for all
-  // eight waves (cinp a multiple of 64).  PTK_CONV_SPLIT=8 forces it where it applies,
-  // PTK_CONV_S8=0 turns the rule off, PTK_CONV_S8_MAX sets the upper bound in waves (1536).
+  // The 8-way split (8-wave workgroups over the same tiles): for a single problem on 32-row
+  // tiles whose 4-way grid leaves one lone wave on most SIMDs (1 to 1.5 waves per SIMD), it
+  // doubles the waves that hide each other's latency at the cost of twice the partial sums.  On
+  // 16-row tiles, which already do more staging and epilogue work per MFMA, it measured no faster
+  // alone and slower batched.  Needs whole chunks for all eight waves (cinp a multiple of 64).
+  // PTK_CONV_SPLIT=8 forces it where it applies, PTK_CONV_S8=0 turns the rule off,
+  // PTK_CONV_S8_MAX sets the upper bound in waves (1536).
   const bool s8_ok = nb == 1 && n == 1 && ds[0]->cinp % (8 * CONV_CK) == 0;
   const long long s8_max = env_knob_or("PTK_CONV_S8_MAX", 1536);
   if (s8_ok && (env_s == 8 || (env_s == 0 && env_knob_or("PTK_CONV_S8", 1) != 0 && best == 4 &&
-                               best_waves >= (long long) kSimds && best_waves < s8_max)))
+                               best_rb == 32 && best_waves >= (long long) kSimds &&
+                               best_waves < s8_max)))
     best = 8;
   *rb_out = best_rb;
   return best;
