@@ -7,7 +7,8 @@
 // reference's packed phase layout), columns are output positions, the reduction runs over
 // (tap, input channel).  im2col never exists: each wave stages a window of input columns per
 // channel chunk in LDS and reads it K times at the K tap shifts.  The four waves of a workgroup
-// split the input channels and reduce through LDS in a fixed order (deterministic), then the
+// (eight for the 8-way split of single problems that leave one wave per SIMD) split the input
+// channels and reduce through LDS in a fixed order (deterministic), then the
 // epilogue (bias, LeakyReLU/ReLU/scalar ops, residual / branch-sum tensor adds, division) is
 // applied on the accumulator values right before the single store.
 #include <hip/hip_runtime.h>
@@ -468,7 +469,7 @@ struct ConvGroup {
   ConvEpi ep[PTK_MAX_GROUP];
   ptk_conv_desc d[PTK_MAX_GROUP];
   int ngroup;
-  int split;                      // waves of a workgroup sharing one output block: 1, 2 or 4
+  int split;                      // waves of a workgroup sharing one output block: 1, 2, 4 or 8
   int lg_split;                   // log2(split)
 };
 
