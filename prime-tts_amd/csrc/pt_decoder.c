@@ -857,31 +857,41 @@ static void aux_destroy(aux_t *a) {
   memset(a, 0, sizeof *a);
 }
 
-static aux_t *aux_get(pt_ctx *c) {
+/* The context's entry, with the streams a split in need + 1 parts uses.  Streams are made when
+ * first needed, never ahead: HIP binds each new stream to the next of its hardware queues in
+ * turn, so streams made early would shift the queues the contexts made after them land on (nine
+ * contexts each made with three extra streams put every context stream on one queue, and the
+ * queue-fed config-5 step took 5.7 against 5.0-5.25 ms).  NULL when any of them cannot be made. */
+static aux_t *aux_get(pt_ctx *c, int need) {
   aux_t *r = NULL;
   pthread_mutex_lock(&g_aux_lock);
   for (int i = 0; i < AUX_MAX && !r; i++)
     if (g_aux[i].c == c) r = &g_aux[i];
   for (int i = 0; i < AUX_MAX && !r; i++) {
     if (g_aux[i].c) continue;
-    aux_t a;
-    memset(&a, 0, sizeof a);
-    a.c = c;
-    int bad = ptk_event_create(&a.fork);
-    for (int k = 0; k < WIN_PARTS_MAX - 1 && !bad; k++)
-      bad = ptk_stream_create(&a.s[k]) || ptk_event_create(&a.join[k]);
-    if (bad) {
+    if (ptk_event_create(&g_aux[i].fork)) {
       PT_LOG("extra streams of a context: %s", ptk_last_error());
-      aux_destroy(&a);
-    } else {
-      g_aux[i] = a;
-      r = &g_aux[i];
+      g_aux[i].fork = NULL;
+      break;
     }
-    break;
+    g_aux[i].c = c;
+    r = &g_aux[i];
   }
+  if (need > WIN_PARTS_MAX - 1) need = WIN_PARTS_MAX - 1;
+  for (int k = 0; r && k < need; k++)
+    if ((!r->s[k] && ptk_stream_create(&r->s[k])) || (!r->join[k] && ptk_event_create(&r->join[k]))) {
+      PT_LOG("extra streams of a context: %s", ptk_last_error());
+      r = NULL;   /* what was made stays in the entry until the context shuts down */
+    }
   pthread_mutex_unlock(&g_aux_lock);
   return r;
 }
+
+static int win_parts(int n);
+
+/* The extra streams the default split uses, made now rather than inside the first long request
+ * a context serves.  Call it once every context of a server is made (see aux_get). */
+void ptdi_aux_prepare(pt_ctx *c) { (void) aux_get(c, win_parts(1 << 20) - 1); }
 
 void ptdi_aux_release(pt_ctx *c) {
   pthread_mutex_lock(&g_aux_lock);
@@ -920,7 +930,7 @@ static int win_batch(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, c
         ? c->g_arena_bytes - al256(c->g_arena_used) : 0;
     if (need > free_b) parts = 1;
   }
-  aux_t *x = parts > 1 ? aux_get(c) : NULL;
+  aux_t *x = parts > 1 ? aux_get(c, parts - 1) : NULL;
   if (!x) return win_range(c, m, z, T, pl, pl->b0, pl->nfull, win, ctx, wav);
   /* the extra streams start after everything queued on the context's stream so far */
   if (ptk_event_record(x->fork, c->g_stream)) return -1;
@@ -1102,6 +1112,7 @@ ptd_server *ptd_server_create(int nctx, size_t arena_bytes) {
     }
   }
   s->n = nctx;
+  for (int i = 0; i < nctx; i++) ptdi_aux_prepare(&s->ctx[i]);   /* after every context stream */
   return s;
 }
 

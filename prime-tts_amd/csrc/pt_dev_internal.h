@@ -62,10 +62,12 @@ int ptdi_ctx_init(pt_ctx *c, size_t arena_bytes, int verbose);
 /* elapsed wall-clock ms since an arbitrary origin */
 double ptdi_now_ms(void);
 
+/* make / release the extra streams a context's windowed decodes split long batched runs over
+ * (pt_decoder.c; made on first use when not prepared) */
+void ptdi_aux_prepare(pt_ctx *c);
+void ptdi_aux_release(pt_ctx *c);
 /* windowed decode with the reference's first / later widths; t_first != NULL: window 0 is
  * decoded alone, waited for, and its completion time stored there */
-/* releases the second stream a context's windowed decodes may have made (pt_decoder.c) */
-void ptdi_aux_release(pt_ctx *c);
 int ptdi_decode_windows(pt_ctx *c, const struct ptd_model *m, const float *z, int64_t T,
                         int win_first, int win, int ctx, float *wav, double *t_first);
 

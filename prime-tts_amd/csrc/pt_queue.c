@@ -150,6 +150,8 @@ ptd_queue *ptd_queue_create(const ptd_model *m, int nworkers, size_t arena_bytes
       return NULL;
     }
   }
+  /* after every worker's stream: a worker's first long-form job then makes no streams */
+  for (int i = 0; i < nworkers; i++) ptdi_aux_prepare(&q->ctx[i]);
   for (int i = 0; i < nworkers; i++) {
     q->args[i] = (qworker_arg){q, i};
     if (pthread_create(&q->th[i], NULL, qworker, &q->args[i])) {
