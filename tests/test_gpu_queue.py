@@ -209,6 +209,40 @@ def test_queue_staggered_submissions(env):
             dz.free(); dw.free()
 
 
+@pytest.mark.parametrize("parts_env", [("PTD_WINDOW_PARTS", "4"), ("PTD_WINDOW_STREAMS", "1"),
+                                       ("PTD_WINDOW_STREAMS", "2")])
+def test_queue_window_split_beyond_prepared_streams(env, parts_env, monkeypatch):
+    """The queue makes each worker's extra stream for the default two-part split when it is
+    created.  A split in four parts asked for afterwards makes the two more streams it needs on
+    first use. Keeping every run on one stream, or splitting every run in two, works on the same
+    prepared workers.  Each output equals the one-stream windowed decode bit for bit."""
+    ctx, model = env
+    lib = ctx.lib
+    T, seed, wf, w, cx = 2600, 77, 48, 96, 16   # 39 full windows: four parts of at least 8
+    say(f"queue: window split with {parts_env[0]}={parts_env[1]} after the queue is made")
+    monkeypatch.delenv("PTD_WINDOW_PARTS", raising=False)
+    monkeypatch.delenv("PTD_WINDOW_STREAMS", raising=False)
+    arena = int(lib.ptd_windows2_arena_bytes(T, wf, w, cx)) + (16 << 20)
+    monkeypatch.setenv("PTD_WINDOW_STREAMS", "1")
+    ref = _expected(ctx, model, (T, seed, wf, w, cx, 0.0))
+    monkeypatch.delenv("PTD_WINDOW_STREAMS")
+    q = lib.ptd_queue_create(model.ptr, 2, arena, 8)
+    assert q
+    monkeypatch.setenv(*parts_env)
+    bufs, jobs = _jobs(ctx, [(T, seed, wf, w, cx, 0.0), (T, seed, wf, w, cx, 1.0)])
+    try:
+        ids = [lib.ptd_queue_submit(q, C.byref(j)) for j in jobs]
+        assert min(ids) >= 0
+        for k, i in enumerate(ids):
+            s = pkg.JobStatus()
+            assert lib.ptd_queue_wait(q, i, C.byref(s)) == 0 and s.rc == 0
+            assert np.array_equal(bufs[k][1].download(ctx), ref), k
+    finally:
+        lib.ptd_queue_destroy(q)
+        for dz, dw in bufs:
+            dz.free(); dw.free()
+
+
 def test_queue_refusals_and_drain_on_destroy(env):
     ctx, model = env
     lib = ctx.lib
