@@ -78,7 +78,10 @@ class EventTimer:
         self.lib, self.ctx = pkg.load(), ctx
         self.e0, self.e1 = self.lib.ptd_event_create(), self.lib.ptd_event_create()
 
-    def time(self, fn, reps):
+    def time(self, fn, reps, warmup=0):
+        """ms per call of fn over reps calls, after warmup untimed calls on the same stream."""
+        for _ in range(warmup):
+            fn()
         self.lib.ptd_event_record(self.ctx.ptr, self.e0)
         for _ in range(reps):
             fn()
@@ -561,23 +564,22 @@ def main():
     z226 = pkg.synth.latent(226, 226)
     dz = pkg.DevBuf.of(ctx, z226)
     dh = pkg.DevBuf(512 * 226)
+    # single launches: 20 untimed calls first, so the timed 100 run at the clock a sustained
+    # stream of them gets (the first tens of launches of a layer run a few % slower)
     f1 = lambda: lib.ptd_layer(ctx.ptr, model.ptr, 0, dz.ptr, 226, 1, dh.ptr, 0.0, 0.1)  # noqa: E731
-    f1()
-    ms = timer.time(f1, 50)
+    ms = timer.time(f1, 100, warmup=20)
     cfg["config1_conv_tflops"] = round(2 * 512 * 192 * 7 * 226 / (ms * 1e-3) / 1e12, 3)
     cfg["config1_frac"] = round(cfg["config1_conv_tflops"] / MFMA_F32_PEAK, 4)
     dx0 = pkg.DevBuf(256 * 904)
     f2 = lambda: lib.ptd_layer(ctx.ptr, model.ptr, 1, dh.ptr, 226, 1, dx0.ptr, 0.1, 0.0)  # noqa: E731
-    f2()
-    ms = timer.time(f2, 50)
+    ms = timer.time(f2, 100, warmup=20)
     cfg["config2_convT_tflops"] = round(2 * 256 * 512 * 4 * 904 / (ms * 1e-3) / 1e12, 3)
     cfg["config2_frac"] = round(cfg["config2_convT_tflops"] / MFMA_F32_PEAK, 4)
     for stage, (C_, T) in enumerate([(256, 904), (128, 3616)]):
         x = pkg.DevBuf.of(ctx, np.random.default_rng(5).standard_normal((C_, T)).astype(np.float32))
         y = pkg.DevBuf(C_ * T)
         f3 = lambda: lib.ptd_mrf(ctx.ptr, model.ptr, stage, x.ptr, T, 0.1, y.ptr)  # noqa: E731
-        f3()
-        ms = timer.time(f3, 20)
+        ms = timer.time(f3, 20, warmup=3)
         # 3 dilations x (c1 + c2) x branches K 3 + 7 + 11 = 126 tap-weighted convs of C x C
         cfg[f"config3_mrf{C_}_tflops"] = round(2 * C_ * C_ * T * 126 / (ms * 1e-3) / 1e12, 3)
         cfg[f"config3_mrf{C_}_frac"] = round(cfg[f"config3_mrf{C_}_tflops"] / MFMA_F32_PEAK, 4)
