@@ -524,8 +524,9 @@ __device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, unsigned vof
 // eighths/quarters/halves of the input channels (S = 1: each wave its own block over all channels)
 // and are reduced through LDS in wave order (deterministic).  NW = 8 runs S = 8 only.  KT > 0:
 // every problem of the group has K <= KT and the whole next chunk's A operands (KT float4 / float2
-// per lane) are prefetched while the current chunk runs; KT == 0: any K, A loaded per tap.  IN: input transform (PTK_IN_*).  RB: rows per tile, 32 (32x32x2 MFMA,
-// weights from d.w) or 16 (16x16x4 MFMA on two 16-column blocks, weights from d.w16).
+// per lane) are prefetched while the current chunk runs; KT == 0: any K, A loaded per tap.  IN:
+// input transform (PTK_IN_*).  RB: rows per tile, 32 (32x32x2 MFMA, weights from d.w) or 16
+// (16x16x4 MFMA on two 16-column blocks, weights from d.w16).
 template <int KT, int NB, int IN, int RB, int NW>
 __global__ void __launch_bounds__(64 * NW) conv_mfma_kernel(const ConvGroup g) {
   extern __shared__ float smem[];
