@@ -301,13 +301,15 @@ def sndr_db(est, ref):
     return float("inf") if err == 0.0 else float(10.0 * np.log10(float(np.sum(ref ** 2)) / err))
 
 
-def cpu_baseline(pkg, gpu_wavs=None):
+def cpu_baseline(pkg, gpu_wavs=None, gpu_long=None):
     """The reference's own CPU conv path (oracle/_ref, built from the reference sources) inside the
     oracle's decoder driver, or the C restatement when _ref is absent.  Timed two ways: config 5's
     eight requests as eight host threads pinned to eight distinct cores (the reference's
     one-thread-per-stream model, main_v21_par.c:134-140), and one config-4 request on one thread.
     gpu_wavs: the same eight requests' waveforms from the timed GPU step, compared (SNDR) with the
-    CPU ones."""
+    CPU ones.  gpu_long: the timed step's stitched long-form windows (T = 1500, 96/16), compared
+    with one full decode of the same latents on the same CPU path, its conv nodes split over the
+    host's threads (bit-identical to one thread; untimed)."""
     sys.path.insert(0, str(ROOT / "tests"))
     import oracle_lib as ol
     ws, bs = pkg.synth.decoder_weights(1234)
@@ -329,6 +331,12 @@ def cpu_baseline(pkg, gpu_wavs=None):
     audio1 = T * HOP / SR
     layers = _cpu_layers(pkg, ol, ws, bs, use_ref, cores[0])
     mm = _cpu_matmul(ol) if use_ref else None
+    long_db = None
+    if gpu_long is not None:
+        T_long = gpu_long.size // HOP
+        ref_long = ol.decoder(ws, bs, pkg.synth.latent(T_long, 900 + 8), use_ref=use_ref,
+                              threads=ol.host_threads())
+        long_db = round(sndr_db(gpu_long, ref_long), 2)
     return {"value": round(audio8 / dt8, 4), "unit": "audio-s/s", "cores": nthr, "kind": kind,
             "sample": f"config 5's 8 requests (T={Ts}, {audio8:.2f} s audio; the T=1500 long-form "
                       f"request not included) as {nthr} threads pinned to cores {cores[:nthr]}: "
@@ -341,7 +349,8 @@ def cpu_baseline(pkg, gpu_wavs=None):
             "host_cpus": len(cores), "nproc": os.cpu_count(), "model": _cpu_model(),
             # the same requests' waveforms from the timed GPU step against these CPU ones
             "sndr_vs_gpu_db": [round(sndr_db(g, c), 2) for g, c in zip(gpu_wavs, cpu_wavs)]
-            if gpu_wavs is not None else None}
+            if gpu_wavs is not None else None,
+            "longform_sndr_vs_gpu_db": long_db}
 
 
 MATMUL_SHAPES = [(37, 53, 29), (120, 192, 120), (120, 96, 192)]   # m, k, n: encoder attention
@@ -808,9 +817,11 @@ def main():
     out["parity"] = parity
     if not args.no_cpu_baseline:
         log("cpu baseline (reference conv path: 8 pinned threads, then 1 thread for config 4 and configs 1-3) ...")
-        out["cpu_baseline"] = cpu_baseline(pkg, c5_wavs[:8])
+        out["cpu_baseline"] = cpu_baseline(pkg, c5_wavs[:8], c5_wavs[-1])
         snd = out["cpu_baseline"].pop("sndr_vs_gpu_db")
         parity["config5_requests_vs_reference_cpu_sndr_db"] = {"min": min(snd), "per_request": snd}
+        parity["config5_longform_windows_vs_reference_cpu_full_decode_sndr_db"] = \
+            out["cpu_baseline"].pop("longform_sndr_vs_gpu_db")
     log(f"parity: {parity}")
     timer.close()
     model.close()

@@ -88,9 +88,13 @@ size_t ptd_decode_arena_bytes(int64_t T, int batch);
  * static device scratch of the library (64 MiB per GPU, held until the process ends) instead of
  * the context's arena.  It allocates nothing.  A decode needing more than the scratch
  * (ptd_decode_arena_bytes(T, batch) > 64 MiB, e.g. batch 1 above 435 frames) is refused: -1 and a
- * stderr line, nothing queued.  Every call on one GPU shares that GPU's scratch: calls that
- * overlap in time on one GPU (other contexts' streams) race and must be serialised by the caller;
- * calls on one stream are ordered.  Same output bits as ptd_decode.  Asynchronous.  0 / -1. */
+ * stderr line, nothing queued.  Every call on one GPU shares that GPU's scratch.  Eager calls are
+ * ordered on the GPU by the library: each call's kernels wait for those of the previous call on
+ * that GPU, whichever context's stream ran it (an event per GPU, made at set-up), so contexts may
+ * call one after another without synchronising.  A call made while its stream is being captured
+ * records no such wait: replays of the graph race with any other use of the scratch that overlaps
+ * them in time, and the caller orders them (one stream for all of them, or a synchronisation in
+ * between).  Same output bits as ptd_decode.  Asynchronous.  0 / -1. */
 int ptd_decode_noalloc(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int batch,
                        float *wav);
 /* Same, also copying the six stage tensors (conv_pre+leaky, ups.0, MRF-256 out, ups.1, MRF-128
@@ -130,17 +134,19 @@ int ptd_mrf_depth(pt_ctx *c, const ptd_model *m, int stage, int depth, const flo
                   const float *const *xin_leaky, float *const *a, float *const *y,
                   float *const *y_leaky, int64_t T);
 
-/* Long-form request through overlap-save windows (config 5; the reference's streaming driver,
- * main_v21_serve.c:210-264 with pt_v21_host.c:2749-2912): frames [a - ctx, a + hop + ctx) are
- * decoded per window (clipped to the sequence) and the samples of frames [a, a + hop) are kept,
- * hop = win - 2*ctx.  All windows are independent, so they run as one batched decode.
- * z [192][T], wav [256*T].  Asynchronous. */
+/* Long-form request through overlap-save windows (config 5; the reference's --stream driver,
+ * main_v21.c:331-370 with pt_v21_host.c:2789-2912): window k decodes frames [k*hop, k*hop + win)
+ * clipped to the sequence, hop = win - 2*ctx, and keeps the samples of its frames [ctx, win - ctx)
+ * (from 0 in the first window, to its end in the last).  win >= 2*ctx + 1, taken as given.  All
+ * windows are independent, so they run as one batched decode.  z [192][T], wav [256*T].
+ * Asynchronous. */
 int ptd_decode_windows(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int win, int ctx,
                        float *wav);
 size_t ptd_windows_arena_bytes(int64_t T, int win, int ctx);
 /* The same with the reference's streaming schedule (main_v21_serve.c:219-257): the first window
  * win_first frames wide (fast first audio; the reference's default 48), the later ones win (its
- * default 256), both >= 2*ctx + 1.  The first window runs as its own decode when its width
+ * default 256); a width below 2*ctx + 8 is raised to it, as the reference server does
+ * (main_v21_serve.c:223-224).  The first window runs as its own decode when its width
  * differs, the evenly spaced full windows as one batched decode, a clipped last window alone.
  * Output identical to decoding the windows one at a time (ptd_decode_chunk) and keeping what the
  * reference's loop keeps.  Asynchronous.  0 / -1. */

@@ -11,6 +11,7 @@
 #include "pt_oracle.h"
 
 #include <math.h>
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -233,6 +234,77 @@ void orc_set_conv_impl(orc_conv_fn conv, orc_convT_fn convT) {
   g_convT = convT ? convT : orc_convT;
 }
 
+/* ------------------------------------------------------------------ node threading
+ * A batch-1 conv or convT node may be split over its output-channel quads across host threads
+ * (orc_set_threads).  Every output row is then summed by one thread, in the same order as in the
+ * one-thread run, through the same conv function on a slice of the packed weights (a convT's
+ * phase rows r*C4/4 + q are gathered per slice), so the results are bit-identical and only the
+ * wall time changes.  Tests use it to decode long sequences; the CPU baseline keeps one thread
+ * per request. */
+static int g_threads = 1;
+
+void orc_set_threads(int n) { g_threads = n < 1 ? 1 : (n > 64 ? 64 : n); }
+int orc_get_threads(void) { return g_threads; }
+
+typedef struct {
+  int is_convT;
+  const float *x;
+  int64_t ldx, cin, tin, ldy, n;
+  float *y;
+  int cout, K, s, pad, dil, epi0, q0, q1, nq;
+  const float *w, *b;
+  float a0;
+  int rc;
+} node_part;
+
+static void *node_part_run(void *arg) {
+  node_part *p = arg;
+  const int co0 = 4 * p->q0, cout = (p->cout < 4 * p->q1 ? p->cout : 4 * p->q1) - co0;
+  float *y = p->y + (int64_t) co0 * p->ldy;
+  const float *b = p->b ? p->b + co0 : NULL;
+  if (!p->is_convT) {
+    const float *w = p->w + (int64_t) p->q0 * p->K * p->cin * 4;
+    p->rc = g_conv(p->x, p->ldx, p->cin, y, p->ldy, p->n, cout, p->K, 1, p->pad, p->dil, w, b, 1,
+                   p->epi0, 0, p->a0, 0.0f);
+    return NULL;
+  }
+  const int ntap = (p->K + p->s - 1) / p->s, nqs = p->q1 - p->q0;
+  const int64_t quad = (int64_t) ntap * p->cin * 4;
+  float *w = malloc((size_t) (p->s * nqs * quad) * sizeof(float));
+  if (!w) { p->rc = -1; return NULL; }
+  for (int r = 0; r < p->s; r++)
+    memcpy(w + r * nqs * quad, p->w + ((int64_t) r * p->nq + p->q0) * quad,
+           (size_t) (nqs * quad) * sizeof(float));
+  p->rc = g_convT(p->x, p->ldx, p->cin, p->tin, y, p->ldy, cout, p->s, p->pad, p->K, w, b, 1);
+  free(w);
+  return NULL;
+}
+
+/* runs the node's quads [0, nq) in up to g_threads contiguous slices; 1 when it ran, 0 when the
+ * node is left to the caller (one thread, or too few quads), -1 on failure */
+static int node_threads(node_part proto) {
+  int parts = g_threads < proto.nq ? g_threads : proto.nq;
+  if (parts < 2) return 0;
+  node_part p[64];
+  pthread_t th[64];
+  int started = 0, rc = 1;
+  for (int i = 0; i < parts; i++) {
+    p[i] = proto;
+    p[i].q0 = (int) ((int64_t) proto.nq * i / parts);
+    p[i].q1 = (int) ((int64_t) proto.nq * (i + 1) / parts);
+    p[i].rc = -1;
+  }
+  for (int i = 1; i < parts; i++) {
+    if (pthread_create(&th[i], NULL, node_part_run, &p[i])) break;
+    started = i;
+  }
+  node_part_run(&p[0]);
+  for (int i = 1; i <= started; i++) pthread_join(th[i], NULL);
+  for (int i = 0; i < parts; i++)
+    if (p[i].rc != 0) rc = -1;
+  return rc;
+}
+
 /* one conv node as the interpreter runs it on the CPU path: padded scratch, conv, trim */
 static int conv_node(const float *x, int64_t T, int cin, int cout, int K, int pad, int dil,
                      const float *w, const float *b, int epi0, float a0, float *y, int64_t batch) {
@@ -243,7 +315,13 @@ static int conv_node(const float *x, int64_t T, int cin, int cout, int K, int pa
   float *yp = c4 == cout ? y : malloc((size_t) (batch * c4 * Tout) * sizeof(float));
   if (!xp || !yp) { free(xp); if (yp != y) free(yp); return -1; }
   orc_pad_rows(x, batch, cin, T, pad, xp);
-  g_conv(xp, ld, cin, yp, Tout, Tout, cout, K, 1, pad, dil, w, b, batch, epi0, 0, a0, 0.0f);
+  const node_part np = {.x = xp, .ldx = ld, .cin = cin, .ldy = Tout, .n = Tout, .y = yp,
+                        .cout = cout, .K = K, .pad = pad, .dil = dil, .epi0 = epi0, .nq = c4 / 4,
+                        .w = w, .b = b, .a0 = a0};
+  const int tr = batch == 1 ? node_threads(np) : 0;
+  if (tr < 0) { free(xp); if (yp != y) free(yp); return -1; }
+  if (tr == 0)
+    g_conv(xp, ld, cin, yp, Tout, Tout, cout, K, 1, pad, dil, w, b, batch, epi0, 0, a0, 0.0f);
   if (yp != y) {
     for (int64_t bb = 0; bb < batch; bb++)
       memcpy(y + bb * cout * Tout, yp + bb * c4 * Tout, (size_t) (cout * Tout) * sizeof(float));
@@ -260,7 +338,12 @@ static int convT_node(const float *x, int64_t tin, int cin, int cout, int K, int
   const int c4 = (cout + 3) / 4 * 4;
   float *yp = c4 == cout ? y : malloc((size_t) (batch * c4 * Lout) * sizeof(float));
   if (!yp) return -1;
-  g_convT(x, tin, cin, tin, yp, Lout, cout, s, pad, K, w, b, batch);
+  const node_part np = {.is_convT = 1, .x = x, .ldx = tin, .cin = cin, .tin = tin, .ldy = Lout,
+                        .y = yp, .cout = cout, .K = K, .s = s, .pad = pad, .nq = c4 / 4, .w = w,
+                        .b = b};
+  const int tr = batch == 1 ? node_threads(np) : 0;
+  if (tr < 0) { if (yp != y) free(yp); return -1; }
+  if (tr == 0) g_convT(x, tin, cin, tin, yp, Lout, cout, s, pad, K, w, b, batch);
   if (yp != y) {
     for (int64_t bb = 0; bb < batch; bb++)
       memcpy(y + bb * cout * Lout, yp + bb * c4 * Lout, (size_t) (cout * Lout) * sizeof(float));

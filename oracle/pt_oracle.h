@@ -41,6 +41,13 @@ typedef int (*orc_convT_fn)(const float *, int64_t, int64_t, int64_t, float *, i
                             int, const float *, const float *, int64_t);
 void orc_set_conv_impl(orc_conv_fn conv, orc_convT_fn convT);
 
+/* Host threads per batch-1 conv / convT node of the decoder and MRF drivers (default 1): the
+ * node's output-channel quads are split into contiguous slices, one thread each.  Each output is
+ * still summed by one thread in the reference's order, so results are bit-identical to one
+ * thread.  Process-wide; set it while no decoder call runs. */
+void orc_set_threads(int n);
+int orc_get_threads(void);
+
 /* The interpreter's padded-row scratch for a conv node (pt_v21_host.c:3274-3281):
  * out[b][ci][pad + t] = X[b][ci][t], zero margins; out has rows of T + 2*pad. */
 void orc_pad_rows(const float *X, int64_t batch, int64_t cin, int64_t T, int pad, float *out);

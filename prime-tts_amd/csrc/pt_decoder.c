@@ -618,7 +618,9 @@ int ptd_decode(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int bat
  * context's arena: nothing is allocated, so a caller that may not allocate device memory (inside
  * a stream capture, a serving loop that forbids it) can decode.  The scratch is shared by every
  * call on the GPU and keeps the last call's contents; every activation is written before it is
- * read, so nothing needs clearing. */
+ * read, so nothing needs clearing.  Calls on one GPU are ordered there: each call's kernels wait
+ * for the previous call's, whichever context's stream that ran on (ptk_scratch_acquire /
+ * _release); a call under stream capture records no such wait. */
 int ptd_decode_noalloc(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int batch,
                        float *wav) {
   if (!c || !c->use_cuda || !m || !z || !wav || T < 1 || batch < 1) return -1;
@@ -636,16 +638,25 @@ int ptd_decode_noalloc(pt_ctx *c, const ptd_model *m, const float *z, int64_t T,
            cap >> 20);
     return -1;
   }
+  if (ptk_scratch_acquire(c->g_stream)) {
+    PT_LOG("ptd_decode_noalloc: %s", ptk_last_error());
+    return -1;
+  }
   void *a0 = c->g_arena;
   const size_t b0 = c->g_arena_bytes, u0 = c->g_arena_used, h0 = c->arena_alloc_bytes;
   c->g_arena = base;
   c->g_arena_bytes = cap;
   c->g_arena_used = 0;
-  const int rc = ptd_decode(c, m, z, T, batch, wav);
+  int rc = ptd_decode(c, m, z, T, batch, wav);
   c->g_arena = a0;
   c->g_arena_bytes = b0;
   c->g_arena_used = u0;
   c->arena_alloc_bytes = h0;
+  /* recorded even after a failure: whatever part of the decode was queued still uses the scratch */
+  if (ptk_scratch_release(c->g_stream, 1)) {
+    PT_LOG("ptd_decode_noalloc: %s", ptk_last_error());
+    rc = -1;
+  }
   return rc;
 }
 
@@ -960,7 +971,7 @@ static int win_batch(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, c
   return rc;
 }
 
-size_t ptd_windows2_arena_bytes(int64_t T, int win_first, int win, int ctx) {
+static size_t windows_arena(int64_t T, int win_first, int win, int ctx) {
   win_plan pl;
   /* the plan with the first window split off needs at least what the merged one needs */
   if (win_plan_make(T, win_first, win, ctx, 1, &pl)) return 0;
@@ -972,8 +983,13 @@ size_t ptd_windows2_arena_bytes(int64_t T, int win_first, int win, int ctx) {
   return b;
 }
 
+size_t ptd_windows2_arena_bytes(int64_t T, int win_first, int win, int ctx) {
+  ptdi_serve_widths(&win_first, &win, ctx);
+  return windows_arena(T, win_first, win, ctx);
+}
+
 size_t ptd_windows_arena_bytes(int64_t T, int win, int ctx) {
-  return ptd_windows2_arena_bytes(T, win, win, ctx);
+  return windows_arena(T, win, win, ctx);
 }
 
 /* The windows of one sequence, in as few launches as the schedule allows.  t_first (optional):
@@ -1008,6 +1024,7 @@ int ptd_decode_windows(pt_ctx *c, const ptd_model *m, const float *z, int64_t T,
 
 int ptd_decode_windows2(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, int win_first,
                         int win, int ctx, float *wav) {
+  ptdi_serve_widths(&win_first, &win, ctx);
   return ptdi_decode_windows(c, m, z, T, win_first, win, ctx, wav, NULL);
 }
 

@@ -66,8 +66,15 @@ double ptdi_now_ms(void);
  * (pt_decoder.c; made on first use when not prepared) */
 void ptdi_aux_prepare(pt_ctx *c);
 void ptdi_aux_release(pt_ctx *c);
-/* windowed decode with the reference's first / later widths; t_first != NULL: window 0 is
- * decoded alone, waited for, and its completion time stored there */
+/* The reference server's window widths (main_v21_serve.c:223-224): a first or later width below
+ * 2*ctx + 8 is raised to it.  ptd_decode_windows2, its arena size and streaming queue jobs take
+ * them; ptd_decode_windows (the --stream driver's form, main_v21.c:341-362) does not. */
+static inline void ptdi_serve_widths(int *win_first, int *win, int ctx) {
+  if (ctx >= 0 && *win_first < 2 * ctx + 8) *win_first = 2 * ctx + 8;
+  if (ctx >= 0 && *win < 2 * ctx + 8) *win = 2 * ctx + 8;
+}
+/* windowed decode with the reference's first / later widths (taken as given); t_first != NULL:
+ * window 0 is decoded alone, waited for, and its completion time stored there */
 int ptdi_decode_windows(pt_ctx *c, const struct ptd_model *m, const float *z, int64_t T,
                         int win_first, int win, int ctx, float *wav, double *t_first);
 

@@ -206,6 +206,7 @@ int64_t ptd_queue_submit(ptd_queue *q, const ptd_job *job) {
   memset(j, 0, sizeof *j);
   j->id = q->next_id++;
   j->job = *job;
+  if (job->win > 0) ptdi_serve_widths(&j->job.win_first, &j->job.win, j->job.ctx);
   j->state = SLOT_QUEUED;
   j->st.order = -1;
   j->st.worker = -1;

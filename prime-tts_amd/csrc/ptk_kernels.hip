@@ -61,15 +61,28 @@ static __device__ __align__(256) unsigned char scratch[PTK_STATIC_SCRATCH_BYTES]
 #define PTK_SCRATCH_MAX_DEVICES 64
 static std::mutex g_scratch_lock;
 static void *g_scratch_ptr[PTK_SCRATCH_MAX_DEVICES];
+// Users of one GPU's scratch are ordered on that GPU: each waits for the work of the one before
+// (an event recorded after it), whatever stream either ran on.  The event is made at set-up with
+// the address; g_scratch_use[dev] is held from the wait until the record, so two host threads
+// cannot both wait on the same predecessor.
+static hipEvent_t g_scratch_done[PTK_SCRATCH_MAX_DEVICES];
+static bool g_scratch_recorded[PTK_SCRATCH_MAX_DEVICES];
+static std::mutex g_scratch_use[PTK_SCRATCH_MAX_DEVICES];
 
-// resolve (once per device) the current device's copy of `scratch`
-static int scratch_resolve(void **out) {
-  int dev = -1;
-  HCHK(hipGetDevice(&dev));
-  if (dev < 0 || dev >= PTK_SCRATCH_MAX_DEVICES) {
-    set_err("static scratch: device %d out of range", dev);
+static int scratch_device(int *dev) {
+  HCHK(hipGetDevice(dev));
+  if (*dev < 0 || *dev >= PTK_SCRATCH_MAX_DEVICES) {
+    set_err("static scratch: device %d out of range", *dev);
     return -1;
   }
+  return 0;
+}
+
+// resolve (once per device, with that device current) the current device's copy of `scratch`
+// and make its ordering event
+static int scratch_resolve(void **out) {
+  int dev = -1;
+  if (scratch_device(&dev)) return -1;
   std::lock_guard<std::mutex> lk(g_scratch_lock);
   if (!g_scratch_ptr[dev]) {
     void *p = nullptr;
@@ -78,6 +91,7 @@ static int scratch_resolve(void **out) {
       set_err("static scratch: hipGetSymbolAddress gave NULL on device %d", dev);
       return -1;
     }
+    if (!g_scratch_done[dev]) HCHK(hipEventCreateWithFlags(&g_scratch_done[dev], hipEventDisableTiming));
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];
@@ -90,6 +104,47 @@ extern "C" int ptk_static_scratch(void **p, size_t *bytes) {
   if (scratch_resolve(p)) return -1;
   *bytes = PTK_STATIC_SCRATCH_BYTES;
   return 0;
+}
+
+static int stream_capturing(hipStream_t st, bool *on) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HCHK(hipStreamIsCapturing(st, &cs));
+  *on = cs != hipStreamCaptureStatusNone;
+  return 0;
+}
+
+extern "C" int ptk_scratch_acquire(void *s) {
+  int dev = -1;
+  void *p;
+  if (scratch_resolve(&p) || scratch_device(&dev)) return -1;
+  g_scratch_use[dev].lock();
+  bool cap = false;
+  hipError_t e = hipSuccess;
+  if (stream_capturing((hipStream_t) s, &cap) == 0) {
+    if (!cap && g_scratch_recorded[dev]) e = hipStreamWaitEvent((hipStream_t) s, g_scratch_done[dev], 0);
+    if (e == hipSuccess) return 0;
+    set_err("hipStreamWaitEvent on the static scratch's event failed: %s", hipGetErrorString(e));
+  }
+  g_scratch_use[dev].unlock();
+  return -1;
+}
+
+extern "C" int ptk_scratch_release(void *s, int recorded_work) {
+  int dev = -1;
+  if (scratch_device(&dev)) return -1;
+  bool cap = false;
+  int rc = stream_capturing((hipStream_t) s, &cap);
+  if (rc == 0 && recorded_work && !cap) {
+    const hipError_t e = hipEventRecord(g_scratch_done[dev], (hipStream_t) s);
+    if (e == hipSuccess) {
+      g_scratch_recorded[dev] = true;
+    } else {
+      set_err("hipEventRecord on the static scratch's event failed: %s", hipGetErrorString(e));
+      rc = -1;
+    }
+  }
+  g_scratch_use[dev].unlock();
+  return rc;
 }
 
 // ------------------------------------------------------------------------------ runtime wrappers
@@ -1500,6 +1555,20 @@ extern "C" int ptk_leaky(const float *a, float *y, int64_t n, float alpha, void 
 // need no barrier), then the waves make one 256-sample block each from all bands' y (phase C).
 // A workgroup loops over tiles (tile, tile + gridDim.x, ...); the next tile's reads are issued as
 // soon as the current tile's are used and arrive while phases B and C run.
+// An angle p (radians) as revolutions in [-1/2, 1/2] for v_sin_f32 / v_cos_f32, whose input
+// domain is |x| <= 256 revolutions and which see only the rounded product p / 2 pi.  Cody and
+// Waite's two-constant reduction (W. J. Cody, W. Waite, Software Manual for the Elementary
+// Functions, 1980): k = rint(p / 2 pi), r = (p - k C1) - k C2 with C1 = fp32(2 pi) and
+// C2 = 2 pi - C1, each step one fused multiply-add, so r carries p's own bits to within a few
+// units of its last place for |p| up to ~1e7.  For |p| < pi, k = 0 and r = p: the result is the
+// plain p / 2 pi.
+__device__ __forceinline__ float rev_of(float p) {
+  const float k = __builtin_rintf(p * 0.159154943f);
+  float r = __builtin_fmaf(-k, 6.28318548f, p);
+  r = __builtin_fmaf(-k, -1.74845553e-7f, r);
+  return r * 0.159154943f;
+}
+
 template <int TOUT>
 struct TailGeo {
   static constexpr int NG = ((TOUT / 4 + 27) / 4 + 16) / 16;   // 16-frame groups per band
@@ -1637,13 +1706,14 @@ __global__ void __launch_bounds__(256) tail_kernel(const float *__restrict__ p, 
       const int tf = t_lo + 16 * c + lm;
       // the hardware transcendentals: v_exp_f32 is 2^x, v_sin_f32 / v_cos_f32 take revolutions
       // (sin(2 pi x)).  The phase pi * sin(p) in revolutions is sin(p) / 2, within [-1/2, 1/2],
-      // so no range reduction is needed; p itself is a conv output of modest size.
+      // so the outer cos / sin need no range reduction.  The inner sin(p) does: p is an
+      // unbounded conv output (reduced by rev_of below).
       const float m0 = __builtin_amdgcn_exp2f(ld[c][0] * 1.44269504f);
-      const float r0 = 0.5f * __builtin_amdgcn_sinf(ld[c][1] * 0.159154943f);
+      const float r0 = 0.5f * __builtin_amdgcn_sinf(rev_of(ld[c][1]));
       const float m1 = __builtin_amdgcn_exp2f(ld[c][2] * 1.44269504f);
-      const float r1 = 0.5f * __builtin_amdgcn_sinf(ld[c][3] * 0.159154943f);
+      const float r1 = 0.5f * __builtin_amdgcn_sinf(rev_of(ld[c][3]));
       const float m8 = __builtin_amdgcn_exp2f(ld[c][4] * 1.44269504f);
-      const float r8 = 0.5f * __builtin_amdgcn_sinf(ld[c][5] * 0.159154943f);
+      const float r8 = 0.5f * __builtin_amdgcn_sinf(rev_of(ld[c][5]));
       float a0 = m0 * __builtin_amdgcn_cosf(r0);
       float a1 = lg == 0 ? m8 * __builtin_amdgcn_cosf(r8) : m0 * __builtin_amdgcn_sinf(r0);
       float a2 = m1 * __builtin_amdgcn_cosf(r1);

@@ -45,6 +45,8 @@ def oracle():
         lib.orc_dec_stage_len.argtypes = [C.c_int, I64]
         lib.orc_dec_stage_len.restype = I64
         lib.orc_set_conv_impl.argtypes = [C.c_void_p, C.c_void_p]
+        lib.orc_set_threads.argtypes = [C.c_int]
+        lib.orc_get_threads.restype = C.c_int
         _oracle = lib
     return _oracle
 
@@ -130,7 +132,36 @@ def dec_weights_struct(ws, bs):
     return st
 
 
-def decoder(ws, bs, z, stages=False, use_ref=False):
+class node_threads:
+    """Context manager: run the oracle's batch-1 conv / convT nodes on n host threads (their
+    output-channel quads split into slices; bit-identical to one thread) inside the block."""
+
+    def __init__(self, n: int):
+        self.n = int(n)
+
+    def __enter__(self):
+        self.prev = oracle().orc_get_threads()
+        oracle().orc_set_threads(self.n)
+        return self
+
+    def __exit__(self, *exc):
+        oracle().orc_set_threads(self.prev)
+        return False
+
+
+def host_threads() -> int:
+    """Threads a test may use for the oracle: the cores this process may run on, at most 16 (the
+    GPU box's CPU share)."""
+    import os
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def decoder(ws, bs, z, stages=False, use_ref=False, threads=None):
+    """The oracle's decoder on z [192][T]: waveform (and the six stage tensors).  threads: host
+    threads per conv node (bit-identical to one; default one)."""
+    if threads is not None and threads > 1:
+        with node_threads(threads):
+            return decoder(ws, bs, z, stages=stages, use_ref=use_ref)
     lib = oracle()
     if use_ref:
         r = ref()
@@ -228,3 +259,41 @@ def constants():
     bs = np.zeros(144, np.float32)
     oracle().orc_dec_constants(fptr(hann), fptr(bc), fptr(bs))
     return hann, bc.reshape(9, 16), bs.reshape(9, 16)
+
+
+def stream_windows(T: int, win: int, ctx: int):
+    """The windows of the reference's overlap-save driver (`--stream WIN CTX`, main_v21.c:341-362):
+    window k starts at a = k * max(win - 2 ctx, 1) and spans w = min(win, T - a) frames; of its
+    256 w samples it keeps [lo, hi): lo = 0 for the first window, else 256 ctx; hi = 256 w for the
+    last window (a + w >= T), else min(256 (w - ctx), 256 w).  Yields (a, w, lo, hi)."""
+    step = max(win - 2 * ctx, 1)
+    a = 0
+    while True:
+        w = min(win, T - a)
+        first, last = a == 0, a + w >= T
+        n = 256 * w
+        lo = 0 if first else 256 * ctx
+        hi = n if last else min(256 * (w - ctx), n)
+        yield a, w, lo, hi
+        if last:
+            return
+        a += step
+
+
+def stream_stitch(decode_window, T: int, win: int, ctx: int) -> np.ndarray:
+    """Stitches decode_window(a, w) -> 256 w samples over stream_windows(T, win, ctx), keeping
+    [lo, hi) of each window in order, as the reference driver's loop copies them."""
+    out = []
+    for a, w, lo, hi in stream_windows(T, win, ctx):
+        pcm = decode_window(a, w)
+        assert pcm.shape == (256 * w,)
+        if hi > lo:
+            out.append(pcm[lo:hi])
+    return np.concatenate(out) if out else np.zeros(0, np.float32)
+
+
+def decoder_stream(ws, bs, z, win: int, ctx: int, threads=None) -> np.ndarray:
+    """The oracle's decoder on each window of the reference's --stream driver, stitched."""
+    T = z.shape[-1]
+    return stream_stitch(lambda a, w: decoder(ws, bs, np.ascontiguousarray(z[:, a:a + w]),
+                                              threads=threads), T, win, ctx)

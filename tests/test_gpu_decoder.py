@@ -170,6 +170,42 @@ def test_tail_alone_vs_oracle(env, L, batch):
     dp.free(); dw.free()
 
 
+PLANTED_PHASES = [100.0, -100.0, 1000.0, -1000.0, 1600.0, -1600.0, 1e4, -1e4, 1e5, -3e5]
+
+
+@pytest.mark.parametrize("scale", [5.0, 20.0, "planted"])
+def test_tail_large_phase_logits_vs_oracle(env, scale):
+    """The phase channels (9..17 of each band's 18) are raw conv outputs, unbounded: at sigma 5 and
+    20, and with planted values up to |p| = 3e5 among sigma-20 logits (the hardware sine's input
+    domain is 256 revolutions, |p| ~ 1608), the tail stays within 1e-4 x RMS of the oracle's
+    double-precision sin.  The magnitude channels keep sigma 0.7 (exp overflows past 88)."""
+    ctx, model, ws, bs = env
+    say(f"tail with phase logits at scale {scale}")
+    L, batch = 1001, 2
+    rng = np.random.default_rng(99)
+    p = 0.7 * rng.standard_normal((batch, 72, L))
+    phase = np.zeros(72, bool)
+    for band in range(4):
+        phase[band * 18 + 9: band * 18 + 18] = True
+    sig = 20.0 if scale == "planted" else scale
+    p[:, phase, :] = sig * rng.standard_normal((batch, int(phase.sum()), L))
+    if scale == "planted":
+        rows = np.flatnonzero(phase)
+        for b in range(batch):
+            for i, v in enumerate(PLANTED_PHASES * 8):
+                p[b, rows[(7 * i + b) % rows.size], (97 * i + 13 * b) % L] = v
+    p = p.astype(np.float32)
+    dp = dev_of(ctx, p)
+    dw = pkg.DevBuf(batch * 16 * (L - 1))
+    assert ctx.lib.ptd_tail(ctx.ptr, model.ptr, dp.ptr, L, batch, dw.ptr) == 0
+    got = dw.download(ctx).reshape(batch, 16 * (L - 1))
+    for i in range(batch):
+        e = relerr(got[i], ol.tail(p[i], ws[40], bs[40]))
+        say(f"  item {i}: max|err|/rms = {e:.3g}")
+        assert e < 1e-4
+    dp.free(); dw.free()
+
+
 @pytest.mark.parametrize("L,batch", [(2, 1), (65, 3), (3617, 2)])
 def test_tail_block_size_gives_the_same_samples(env, L, batch, monkeypatch):
     """The tail kernel's tile size (256, 512 or 1024 samples, chosen from the work; forced here
@@ -683,7 +719,11 @@ def test_config5_as_benchmarked(env):
     single-stream decode bit for bit, each of the 8 requests reaches >= 60 dB against the oracle
     (decoded on host threads, as the reference's parallel driver gates its streams,
     main_v21_par.c:99-109, :142-157), and the long-form request reaches >= 60 dB against one full
-    decode of the same latents."""
+    decode of the same latents.  The long-form request is also gated against the oracle at
+    T = 1500 (its conv nodes split over host threads, bit-identical to one thread): the stitched
+    windows >= 60 dB against the oracle's full decode and against the oracle's own windows stitched
+    by the reference driver's loop, and each of the six stages of ptd_decode_stages at T = 1500
+    within 1e-4 x RMS of the oracle's."""
     ctx, model, ws, bs = env
     lib = ctx.lib
     Ts = synth.request_lengths(5, 8)
@@ -721,6 +761,20 @@ def test_config5_as_benchmarked(env):
     s_long = np_ref.sndr(outs[8], full_long)
     say(f"  long-form windows vs full decode: {s_long:.1f} dB")
     assert s_long >= 60.0
+    say(f"  oracle at T = {T_long} on {ol.host_threads()} host threads")
+    ref_long, ref_st = ol.decoder(ws, bs, zs[-1], stages=True, threads=ol.host_threads())
+    s_or = np_ref.sndr(outs[8], ref_long)
+    say(f"  long-form windows vs the oracle's full decode: {s_or:.1f} dB")
+    assert s_or >= 60.0
+    ref_win = ol.decoder_stream(ws, bs, zs[-1], WIN, CTX, threads=ol.host_threads())
+    s_ow = np_ref.sndr(outs[8], ref_win)
+    say(f"  long-form windows vs the oracle's windows: {s_ow:.1f} dB")
+    assert s_ow >= 60.0
+    _, st_long = _decode(ctx, model, zs[-1], stages=True)
+    for i in range(6):
+        e = relerr(st_long[i], ref_st[i])
+        say(f"  T = {T_long} stage {i}: max|err|/rms = {e:.3g}")
+        assert e < TOL, f"stage {i}"
     refs, _ = ol.decoder_threads(ws, bs, zs[:8], cores=list(range(8)))
     for i in range(8):
         s = np_ref.sndr(outs[i], refs[i])

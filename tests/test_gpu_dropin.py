@@ -136,6 +136,37 @@ def test_reference_driver_gpu_split(model, tmp_path):
     assert alloc + copy + kern + free <= total * 1.05 + 1.0
 
 
+STREAM_FIXTURE = ROOT / "tests" / "golden" / "ref_decoder_ckpt_T198.npz"
+
+
+@pytest.mark.parametrize("win,cx", [(96, 16), (48, 16)])
+def test_reference_stream_driver_through_the_library(model, tmp_path, win, cx):
+    """The reference's overlap-save streaming path (`--stream WIN CTX`: pt_v21_stream_open runs
+    the encoder once, then pt_v21_stream_chunk the decoder's convs and convTs on each window,
+    main_v21.c:331-370, pt_v21_host.c:2789-2902) with the library as its device: the stitched
+    waveform against what the reference's CPU build stitched on the same 97-token case
+    (tests/golden/ref_decoder_ckpt_T198.npz, written by tests/golden/gen_decoder_ckpt.py on the
+    same container and case), >= 60 dB and closer to it than to the full decode."""
+    d, case, cpu_wav = model
+    g = np.load(STREAM_FIXTURE)
+    if int(np.load(case / "x_lengths.npy")[0]) != int(g["n_tokens"]):
+        pytest.skip("the streamed fixture is the 97-token case")
+    say(f"reference driver --stream {win} {cx} through the library")
+    r = _run([DEV_BIN, "--container", d / "model.ptk", "--case", case, "--out", tmp_path / "s.npy",
+              "--stream", win, cx], 300)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    got = np.load(tmp_path / "s.npy").ravel()
+    full = np.load(cpu_wav).ravel()
+    assert np.array_equal(full, g["wav"])   # the same container and case as the fixture
+    ref = g[f"stream_{win}_{cx}"]
+    assert got.shape == ref.shape
+    s_stream, s_full = np_ref.sndr(got, ref), np_ref.sndr(got, full)
+    say(f"stream {win}/{cx}: {s_stream:.1f} dB vs the CPU build's stream, {s_full:.1f} dB vs its full decode")
+    assert s_stream >= 60.0 and s_stream >= s_full + 20.0
+    m = re.search(r"conv=(\d+) convT=(\d+) matmul=(\d+)", r.stdout)
+    assert m and int(m.group(1)) > 0 and int(m.group(2)) > 0, r.stdout
+
+
 @pytest.mark.skipif(not PAR_BIN.exists(), reason="oracle/_ref/pt_v21_par_mi355x not built")
 @pytest.mark.parametrize("wait", [{}, {"PT_V21_WAIT_US": "200"},
                                   {"PT_V21_WAIT_US": "200", "PT_V21_WAIT_ADAPT": "0"}],

@@ -54,9 +54,11 @@ def _decode(ctx, model, z):
 
 
 def _stream_loop(ctx, model, z, win_first, win, cx):
-    """The reference's synth_stream loop (main_v21_serve.c:226-257), one window at a time."""
+    """The reference's synth_stream loop (main_v21_serve.c:219-257), one window at a time, with
+    its widths raised to at least 2*ctx + 8 (:223-224)."""
     lib = ctx.lib
     T = z.shape[-1]
+    win_first, win = max(win_first, 2 * cx + 8), max(win, 2 * cx + 8)
     dz = pkg.DevBuf.of(ctx, z)
     pcm = pkg.DevBuf(HOP * max(win_first, win))
     n = C.c_int64()
@@ -82,7 +84,8 @@ def _stream_loop(ctx, model, z, win_first, win, cx):
 
 
 @pytest.mark.parametrize("T,wf,w,cx", [(1500, 48, 256, 16), (300, 48, 256, 16), (200, 48, 96, 16),
-                                       (40, 48, 256, 16), (600, 96, 96, 16), (260, 48, 256, 16)])
+                                       (40, 48, 256, 16), (600, 96, 96, 16), (260, 48, 256, 16),
+                                       (300, 36, 96, 16), (200, 36, 36, 16)])
 def test_windows2_matches_the_reference_stream_loop(env, T, wf, w, cx):
     ctx, model = env
     lib = ctx.lib

@@ -159,3 +159,16 @@ def test_one_column_less_poisons(lib, model, pkg, launch, side):
     plan[launch, 1] -= 1
     wav = masked_decoder(raw, bs, z, plan, "mid")
     assert not np.all(np.isfinite(wav[lo:hi]))
+
+
+def test_server_widths_raised_to_two_ctx_plus_eight(lib):
+    """ptd_decode_windows2 (the reference server's schedule) raises a first or later width below
+    2*ctx + 8 to it (main_v21_serve.c:223-224), so its arena need equals that of the raised widths;
+    ptd_decode_windows (the --stream driver's form, which takes win as given) does not."""
+    T, cx = 300, 16
+    low, raised = 2 * cx + 4, 2 * cx + 8
+    a_low = lib.ptd_windows2_arena_bytes(T, low, 96, cx)
+    assert a_low > 0 and a_low == lib.ptd_windows2_arena_bytes(T, raised, 96, cx)
+    assert lib.ptd_windows2_arena_bytes(T, low, low, cx) == lib.ptd_windows2_arena_bytes(T, raised, raised, cx)
+    assert lib.ptd_windows_arena_bytes(T, low, cx) != lib.ptd_windows_arena_bytes(T, raised, cx)
+    assert lib.ptd_windows_arena_bytes(T, 2 * cx, cx) == 0   # below 2*ctx + 1: refused
