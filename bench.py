@@ -266,31 +266,97 @@ def layer_table(csv_path, batch, counter_csv=None):
 def abi_leg(pkg, lib, ctx, model, ws, bs, T=226, reps=5):
     """Config 4's request through the reference ABI with host buffers (tests/abi_decoder.py: the
     decoder's 38 convs and 2 upsampling convTs as pt_v21_conv / pt_v21_convT calls on host arrays,
-    driven the way the reference's interpreter drives the library).  Every call copies its input
-    up and its output back and waits: the PCIe-inclusive per-call path, reported beside the value,
-    never as it.  conv_post's output is compared with the device-resident decoder's
-    (ptd_decode_stages) on the same latents."""
+    driven the way the reference's interpreter drives the library), in three of the interpreter's
+    modes: per call (every call copies its input up and its output back and waits), chained (the
+    interpreter's default conv -> conv chains: c1 results stay on the device for c2) and resident
+    (PT_V21_DEVADD: residual adds, LeakyReLUs and branch sums on device buffers as well).  Each
+    request's wall time splits into the time inside library calls and the Python glue's between
+    them.  The PCIe-inclusive per-call path, reported beside the value, never as it.  conv_post's
+    output is compared with the device-resident decoder's (ptd_decode_stages) on the same
+    latents."""
     sys.path.insert(0, str(ROOT / "tests"))
     import abi_decoder
-    run = abi_decoder.AbiDecoder(pkg, ctx, ws, bs)
     z = pkg.synth.latent(T, 77)
-    p = run.request(z)
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        run.request(z)
-        times.append(time.perf_counter() - t0)
-    ms = float(np.median(times)) * 1e3
     pd = abi_decoder.device_conv_post(pkg, ctx, model, z)
-    run.close()
-    rel = float(np.max(np.abs(p.astype(np.float64) - pd)) / np.sqrt(np.mean(pd.astype(np.float64) ** 2)))
-    return {"frames": T, "conv_calls": run.calls[0] // (reps + 1), "convT_calls": run.calls[1] // (reps + 1),
-            "ms_per_request": round(ms, 3),
-            "audio_s_per_s": round(T * HOP / SR / (ms * 1e-3), 2),
-            "conv_post_vs_device_decoder_max_abs_over_rms": float(f"{rel:.3g}"),
-            "path": "decoder convs / convTs through pt_v21_conv / pt_v21_convT on host buffers "
-                    "(weights pool-resident, c1 + conv_pre LeakyReLU as epilogue code 1, host "
-                    "glue in numpy); tail not included"}
+    rms = np.sqrt(np.mean(pd.astype(np.float64) ** 2))
+    out = {"frames": T, "path": "decoder convs / convTs through pt_v21_conv / pt_v21_convT on host "
+                                "buffers (weights pool-resident, c1 + conv_pre LeakyReLU as "
+                                "epilogue code 1, host glue in numpy); tail not included"}
+    for mode in abi_decoder.MODES:
+        run = abi_decoder.AbiDecoder(pkg, ctx, ws, bs, mode=mode)
+        p = run.request(z)
+        times, libs = [], []
+        for _ in range(reps):
+            l0 = run.lib_s
+            t0 = time.perf_counter()
+            run.request(z)
+            times.append(time.perf_counter() - t0)
+            libs.append(run.lib_s - l0)
+        run.close()
+        i = int(np.argsort(times)[len(times) // 2])   # the median request, split
+        ms, lib_ms = times[i] * 1e3, libs[i] * 1e3
+        rel = float(np.max(np.abs(p.astype(np.float64) - pd)) / rms)
+        out[mode] = {"conv_calls": run.calls[0] // (reps + 1), "convT_calls": run.calls[1] // (reps + 1),
+                     "ms_per_request": round(ms, 3), "library_ms": round(lib_ms, 3),
+                     "glue_ms": round(ms - lib_ms, 3),
+                     "audio_s_per_s": round(T * HOP / SR / (ms * 1e-3), 2),
+                     "library_audio_s_per_s": round(T * HOP / SR / (lib_ms * 1e-3), 2),
+                     "conv_post_vs_device_decoder_max_abs_over_rms": float(f"{rel:.3g}")}
+    return out
+
+
+# The drop-in path's narrow late stages, as the reference interpreter hands them to the library
+# for a T = 226 request (ref/v21_graph_trace.txt:4265-4315): the PQMF synthesis FIR (/dec/Conv,
+# 4 -> 1, K 63, over the 31|31-padded upsampled bands: 57918 input columns, 57856 outputs) through
+# pt_v21_conv, and the iSTFT overlap-add (/dec/ConvTranspose, batch 4, 16 -> 1, K 16, s 4: 3617
+# frames -> 14480 samples) through pt_v21_convT.  Both have cout4 = 4 output rows of which one is
+# the channel and three are the layout's padding.
+NARROW_FIR = dict(cin=4, T=57856 + 62, K=63, cout=1)
+NARROW_OLA = dict(batch=4, cin=16, tin=3617, K=16, s=4, cout=1)
+
+
+def narrow_bytes():
+    """Algorithmic HBM bytes of one launch (inputs, weights, the cout4 output rows)."""
+    f, o = NARROW_FIR, NARROW_OLA
+    fir = 4.0 * (f["cin"] * f["T"] + 4 * f["K"] * f["cin"] + 4 * (f["T"] - f["K"] + 1))
+    lout = (o["tin"] - 1) * o["s"] + o["K"]
+    ola = 4.0 * (o["batch"] * o["cin"] * o["tin"] + o["s"] * 4 * (o["K"] // o["s"]) * o["cin"]
+                 + o["batch"] * 4 * lout)
+    return fir, ola
+
+
+def narrow_abi_loop(pkg, lib, ctx, n):
+    """n pt_v21_conv calls at the PQMF FIR's shape and n pt_v21_convT calls at the iSTFT
+    overlap-add's, on host buffers (each call copies, launches the narrow kernel and waits), for a
+    rocprofv3 kernel trace of the two narrow kernels."""
+    f, o = NARROW_FIR, NARROW_OLA
+    rng = np.random.default_rng(5)
+    fp = pkg.fptr
+    x = rng.standard_normal((f["cin"], f["T"])).astype(np.float32)
+    tout = f["T"] - f["K"] + 1
+    y = np.empty((4, tout), np.float32)
+    w = pkg.synth.pack_conv((0.1 * rng.standard_normal((f["cout"], f["cin"], f["K"]))).astype(np.float32))
+    b = np.zeros(f["cout"], np.float32)
+    pad0 = ctx.get_i64("conv_pad_in")
+    ctx.set_i64("conv_pad_in", 0)
+    try:
+        for _ in range(n):
+            if lib.pt_v21_conv(ctx.ptr, fp(x), f["T"], f["cin"], fp(y), tout, tout, f["cout"], f["K"],
+                               1, 0, 1, fp(w), fp(b), 1, -1, -1, 0, 0, 0.0, 0.0) != 0:
+                raise RuntimeError("narrow conv failed")
+    finally:
+        ctx.set_i64("conv_pad_in", pad0)
+    xo = rng.standard_normal((o["batch"], o["cin"], o["tin"])).astype(np.float32)
+    lout = (o["tin"] - 1) * o["s"] + o["K"]
+    yo = np.empty((o["batch"], 4, lout), np.float32)
+    wo = pkg.synth.pack_convtranspose(
+        (0.1 * rng.standard_normal((o["cin"], o["cout"], o["K"]))).astype(np.float32), o["s"])
+    bo = np.zeros(o["cout"], np.float32)
+    for _ in range(n):
+        if lib.pt_v21_convT(ctx.ptr, fp(xo), o["tin"], o["cin"], o["tin"], fp(yo), lout, o["cout"],
+                            o["s"], 0, o["K"], fp(wo), fp(bo), o["batch"], -1, -1) != 0:
+            raise RuntimeError("narrow convT failed")
+    log(f"kernel loop: {n} narrow ABI conv (PQMF FIR) and {n} convT (iSTFT OLA, batch 4) calls done")
 
 
 def sndr_db(est, ref):
@@ -535,6 +601,7 @@ def main():
             ctx.sync()
             tp.free(); tw.free()
             log(f"kernel loop: {args.kernel_loop} tail launches (L {TAIL_L}, batch {tb}) done")
+        narrow_abi_loop(pkg, lib, ctx, args.kernel_loop)
         # calibration for the HBM byte counters: add_kernel over 64 Mi floats reads exactly
         # 512 MiB and writes 256 MiB per launch
         n = 64 << 20

@@ -254,6 +254,11 @@ void ptd_free(void *p);
  * its env knobs only): after `skip` more device allocations of this library succeed, the next n
  * fail as if the device were out of memory.  Process-wide; n = 0 switches it off. */
 void ptd_debug_fail_allocs(int skip, int n);
+/* The library reads its tuning knobs (PTK_CONV_*, PTK_TAIL_*, PTD_WINDOW_*) from the environment
+ * once per process, at first use.  This re-reads them, for tests that change one between calls
+ * (no counterpart in the reference, whose knobs are static caches too).  The reference's operator
+ * knobs (PT_V21_*) keep their read-once behaviour. */
+void ptd_debug_reload_env(void);
 /* Tests of what a decode reads (no counterpart in the reference): every byte of the context's
  * arena set to `byte` on its stream (0xff makes every float NaN, so a column read before any
  * launch wrote it poisons what depends on it).  Synchronous.  0 / -1. */

@@ -96,6 +96,7 @@ _SIGS = {
     "ptd_malloc": (VP, [C.c_size_t]),
     "ptd_free": (None, [VP]),
     "ptd_debug_fail_allocs": (None, [C.c_int, C.c_int]),
+    "ptd_debug_reload_env": (None, []),
     "ptd_debug_fill_arena": (C.c_int, [VP, C.c_int]),
     "ptd_h2d": (C.c_int, [VP, VP, VP, C.c_size_t]),
     "ptd_d2h": (C.c_int, [VP, VP, VP, C.c_size_t]),

@@ -371,10 +371,31 @@ static int cone_plan_make(cone_plan *cp, int64_t T, int batch, const ptk_emit *e
   return 0;
 }
 
-static int cone_enabled(void) {
+/* Windowed-decode knobs (PTD_WINDOW_CONE, PTD_WINDOW_STREAMS, PTD_WINDOW_PARTS): read once per
+ * process, re-read by ptdi_decoder_knobs_reload (tests that change one between calls). */
+static int g_kn_cone = 1, g_kn_streams = 0, g_kn_parts = 2;
+static pthread_once_t g_kn_once = PTHREAD_ONCE_INIT;
+static pthread_mutex_t g_kn_lock = PTHREAD_MUTEX_INITIALIZER;
+static void decoder_knobs_read(void) {
+  pthread_mutex_lock(&g_kn_lock);
   const char *e = getenv("PTD_WINDOW_CONE");
-  return !(e && e[0] == '0');
+  __atomic_store_n(&g_kn_cone, !(e && e[0] == '0'), __ATOMIC_RELAXED);
+  e = getenv("PTD_WINDOW_STREAMS");
+  __atomic_store_n(&g_kn_streams, e ? atoi(e) : 0, __ATOMIC_RELAXED);
+  e = getenv("PTD_WINDOW_PARTS");
+  __atomic_store_n(&g_kn_parts, e ? atoi(e) : 2, __ATOMIC_RELAXED);
+  pthread_mutex_unlock(&g_kn_lock);
 }
+static int decoder_knob(const int *k) {
+  pthread_once(&g_kn_once, decoder_knobs_read);
+  return __atomic_load_n(k, __ATOMIC_RELAXED);
+}
+void ptdi_decoder_knobs_reload(void) {
+  pthread_once(&g_kn_once, decoder_knobs_read);
+  decoder_knobs_read();
+}
+
+static int cone_enabled(void) { return decoder_knob(&g_kn_cone); }
 
 static void cols_apply(ptk_conv_desc *d, const cols_t *c) {
   d->q0 = c->q0;
@@ -916,13 +937,11 @@ void ptdi_aux_release(pt_ctx *c) {
  * windows beside eight other requests): 2 parts +1.0 to +2.8 % against 1 (by box), 3 and 4 parts
  * below 2.  PTD_WINDOW_STREAMS=1 never splits, =2 splits any run of two or more in two. */
 static int win_parts(int n) {
-  const char *e = getenv("PTD_WINDOW_STREAMS");
-  const int k = e ? atoi(e) : 0;
+  const int k = decoder_knob(&g_kn_streams);
   if (k == 1 || n < 2) return 1;
   if (k == 2) return 2;
   if (n < 16) return 1;
-  const char *pe = getenv("PTD_WINDOW_PARTS");
-  int p = pe ? atoi(pe) : 2;
+  int p = decoder_knob(&g_kn_parts);
   if (p > WIN_PARTS_MAX) p = WIN_PARTS_MAX;
   while (p > 2 && n / p < 8) p--;
   return p < 1 ? 1 : p;

@@ -193,6 +193,23 @@ void ptdi_pool_ref(int delta) {
   pthread_mutex_unlock(&P.lock);
 }
 
+/* PT_V21_UP_PAR (read once per process; pt_v21_cuda.cu:167-174): 1 (default) every context
+ * claims records and copies them in parallel; 0 is the reference's serialised bisection endpoint,
+ * where the first context copies every record while holding the pool lock and the others, once
+ * they get the lock, find the copies done. */
+static int g_up_par = 1;
+static pthread_once_t g_up_par_once = PTHREAD_ONCE_INIT;
+static void up_par_read(void) { g_up_par = env_int("PT_V21_UP_PAR", 1) != 0; }
+
+static int pool_upload(pt_ctx *c) {
+  pthread_once(&g_up_par_once, up_par_read);
+  if (g_up_par) return pool_claim_upload(c);
+  pthread_mutex_lock(&P.lock);
+  const int r = pool_claim_upload(c);
+  pthread_mutex_unlock(&P.lock);
+  return r;
+}
+
 int ptdi_pool_load_src(pt_ctx *c, int n, const void *const *host, const size_t *bytes,
                        const unsigned char *isz) {
   if (!c || !c->use_cuda || n <= 0) return -1;
@@ -206,7 +223,7 @@ int ptdi_pool_load_src(pt_ctx *c, int n, const void *const *host, const size_t *
   }
   pthread_mutex_unlock(&P.lock);
   if (r) return -1;
-  return pool_claim_upload(c);
+  return pool_upload(c);
 }
 
 int ptd_pool_load(pt_ctx *c, int n, const void *const *host, const size_t *bytes) {
@@ -367,7 +384,7 @@ int ptdi_ctx_init(pt_ctx *c, size_t arena_bytes, int verbose) {
   }
   const int upload = P.setup;
   pthread_mutex_unlock(&P.lock);
-  if (r == 0 && upload) r = pool_claim_upload(c);
+  if (r == 0 && upload) r = pool_upload(c);
   if (r) {
     /* leave nothing behind: stream, arena and the pool reference taken above */
     pt_v21_cuda_shutdown(c);
@@ -1024,6 +1041,10 @@ void *ptd_malloc(size_t bytes) {
 }
 void ptd_free(void *p) { ptk_free(p); }
 void ptd_debug_fail_allocs(int skip, int n) { ptk_fail_allocs(skip, n); }
+void ptd_debug_reload_env(void) {
+  ptk_knobs_reload();
+  ptdi_decoder_knobs_reload();
+}
 int ptd_debug_fill_arena(pt_ctx *c, int byte) {
   if (!c || !c->use_cuda || !c->g_arena) return -1;
   if (ptk_fill_async(c->g_arena, byte, c->g_arena_bytes, c->g_stream) || ptk_stream_sync(c->g_stream)) {

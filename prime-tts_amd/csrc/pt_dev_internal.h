@@ -66,6 +66,8 @@ double ptdi_now_ms(void);
  * (pt_decoder.c; made on first use when not prepared) */
 void ptdi_aux_prepare(pt_ctx *c);
 void ptdi_aux_release(pt_ctx *c);
+/* re-read the PTD_WINDOW_* knobs from the environment (otherwise read once; pt_decoder.c) */
+void ptdi_decoder_knobs_reload(void);
 /* The reference server's window widths (main_v21_serve.c:223-224): a first or later width below
  * 2*ctx + 8 is raised to it.  ptd_decode_windows2, its arena size and streaming queue jobs take
  * them; ptd_decode_windows (the --stream driver's form, main_v21.c:341-362) does not. */

@@ -57,6 +57,8 @@ int ptk_static_scratch(void **p, size_t *bytes);
  * device's lock; release records the event on s when work was queued (again not under capture)
  * and drops the lock.  Every successful acquire is followed by one release on the same thread.
  * Neither allocates. */
+/* re-read the PTK_* kernel-selection knobs from the environment (otherwise read once) */
+void ptk_knobs_reload(void);
 int ptk_scratch_acquire(void *s);
 int ptk_scratch_release(void *s, int recorded_work);
 

@@ -13,6 +13,7 @@
 // applied on the accumulator values right before the single store.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <mutex>
 
 #include <type_traits>
@@ -165,6 +166,21 @@ extern "C" int ptk_init(void) {
   if (!selected) {
     HCHK(hipSetDevice(0));
     selected = true;
+    // PT_V21_SYNC, the reference's scheduling mode for host waits (pt_v21_cuda.cu:758-764): 0 spin,
+    // 1 blocking, 2 yield (ROCm treats blocking as yield).  Unset: HIP's own choice.  Set once per
+    // process, on the first thread to select the device; on a device already active in this
+    // process (another library made it so) HIP refuses the change, which is ignored here as the
+    // reference ignores it.
+    static std::once_flag sync_once;
+    std::call_once(sync_once, [] {
+      const char *e = getenv("PT_V21_SYNC");
+      if (!e) return;
+      const int mode = atoi(e);
+      const unsigned fl = mode == 0 ? hipDeviceScheduleSpin
+                        : mode == 1 ? hipDeviceScheduleBlockingSync
+                        : mode == 2 ? hipDeviceScheduleYield : 0u;
+      if (fl && hipSetDeviceFlags(fl) != hipSuccess) (void) hipGetLastError();
+    });
     // set-up of the static scratch's address for this device, outside any later stream capture;
     // a failure here is reported by the entry point that needs it (which retries), not by init
     void *p;
@@ -1073,13 +1089,39 @@ static int conv_window(const ptk_conv_desc *d, int nb) {
 }
 static int win_max(int nb) { return nb == 2 ? WinGeo<2>::XWMAX : WinGeo<1>::XWMAX; }
 
-static int env_knob(const char *name) {
-  const char *e = getenv(name);
-  return e ? atoi(e) : 0;
+// Kernel-selection knobs (PTK_*), read from the environment once per process, at the first
+// launch that consults them, not per launch: launches come from many serving threads at once, and
+// getenv is neither cheap nor safe against a concurrent setenv.  ptk_knobs_reload re-reads them
+// (tests that change a knob between calls); each is an atomic int, so a launch running meanwhile
+// sees the old or the new value of each knob.
+enum KnobId {
+  KN_CONV_SPLIT, KN_CONV_RB, KN_CONV_S8, KN_CONV_S8_MAX, KN_CONV_NB, KN_TAIL_OUT, KN_TAIL_GRID,
+  KN_TAIL_XCD, KN_NARROW, KN_COUNT
+};
+static const struct {
+  const char *name;
+  int dflt;
+} kKnobs[KN_COUNT] = {{"PTK_CONV_SPLIT", 0}, {"PTK_CONV_RB", 0},    {"PTK_CONV_S8", 1},
+                      {"PTK_CONV_S8_MAX", 1536}, {"PTK_CONV_NB", 0}, {"PTK_TAIL_OUT", 0},
+                      {"PTK_TAIL_GRID", 0},   {"PTK_TAIL_XCD", 1},  {"PTK_NARROW", 1}};
+static std::atomic<int> g_knob[KN_COUNT];
+static std::once_flag g_knob_once;
+static std::mutex g_knob_lock;
+
+static void knobs_read() {
+  std::lock_guard<std::mutex> lk(g_knob_lock);
+  for (int i = 0; i < KN_COUNT; i++) {
+    const char *e = getenv(kKnobs[i].name);
+    g_knob[i].store(e ? atoi(e) : kKnobs[i].dflt, std::memory_order_relaxed);
+  }
 }
-static int env_knob_or(const char *name, int dflt) {
-  const char *e = getenv(name);
-  return e ? atoi(e) : dflt;
+static int knob(KnobId k) {
+  std::call_once(g_knob_once, knobs_read);
+  return g_knob[k].load(std::memory_order_relaxed);
+}
+extern "C" void ptk_knobs_reload(void) {
+  std::call_once(g_knob_once, knobs_read);
+  knobs_read();
 }
 
 // Tile shape (RB rows, channel split S in {1, 2, 4, 8}; PTK_CONV_RB and PTK_CONV_SPLIT override).
@@ -1115,7 +1157,7 @@ static double split_eff(long long waves, int S) {
   return balance * hide * cost;
 }
 static int choose_tiles(const ptk_conv_desc *const *ds, int n, int nb, int *rb_out) {
-  const int env_s = env_knob("PTK_CONV_SPLIT"), env_rb = env_knob("PTK_CONV_RB");
+  const int env_s = knob(KN_CONV_SPLIT), env_rb = knob(KN_CONV_RB);
   bool rb16_ok = nb == 1 && (n == 1 || env_rb == 16);
   for (int i = 0; i < n; i++)
     if (ds[i]->w16 == nullptr) rb16_ok = false;
@@ -1158,8 +1200,8 @@ static int choose_tiles(const ptk_conv_desc *const *ds, int n, int nb, int *rb_o
   // PTK_CONV_SPLIT=8 forces it where it applies, PTK_CONV_S8=0 turns the rule off,
   // PTK_CONV_S8_MAX sets the upper bound in waves (1536).
   const bool s8_ok = nb == 1 && n == 1 && ds[0]->cinp % (8 * CONV_CK) == 0;
-  const long long s8_max = env_knob_or("PTK_CONV_S8_MAX", 1536);
-  if (s8_ok && (env_s == 8 || (env_s == 0 && env_knob_or("PTK_CONV_S8", 1) != 0 && best == 4 &&
+  const long long s8_max = knob(KN_CONV_S8_MAX);
+  if (s8_ok && (env_s == 8 || (env_s == 0 && knob(KN_CONV_S8) != 0 && best == 4 &&
                                best_rb == 32 && best_waves >= (long long) kSimds &&
                                best_waves < s8_max)))
     best = 8;
@@ -1171,7 +1213,7 @@ static int choose_tiles(const ptk_conv_desc *const *ds, int n, int nb, int *rb_o
 // registers and halve the grid; on MI355X they lost at every decoder shape measured (batch 1 and
 // 8), so they are only used when PTK_CONV_NB=2 asks for them.
 static int choose_nb(const ptk_conv_desc *d) {
-  const int env_nb = env_knob("PTK_CONV_NB");
+  const int env_nb = knob(KN_CONV_NB);
   if (env_nb == 2 && conv_window(d, 2) <= win_max(2)) return 2;
   return 1;
 }
@@ -1347,6 +1389,103 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
 // ------------------------------------------------------------------------------ SIMT fallbacks
 // Narrow problems (the cout = 1..15 convs of the tail, 1-channel inputs): one thread per output,
 // summing over tap then channel onto the bias in the reference's order.
+// ------------------------------------------------------------------------------ narrow convs
+// Convs and convTs with few output rows on the reference ABI path (cout4 < 16: the PQMF synthesis
+// FIR 4 -> 1 K 63; the iSTFT overlap-add 16 -> 1 and window sum 1 -> 1, K 16 s 4; the PQMF x4
+// zero-insert 4 -> 4 K 4 s 4).  A workgroup of NARROW_THREADS threads takes that many consecutive
+// output columns (convT: delay-line steps q, each giving s outputs) of one batch item, stages the
+// input window they read, [cin][win], in LDS once, and each thread computes its column for every
+// real output row.  The weights are read with uniform addresses (scalar loads).  The order per
+// output is the generic kernels' (bias, tap ascending, channel ascending, out-of-range columns
+// skipped), so the results are the same bits.  The layout's padding rows (cout..cout4-1, zero
+// weights and bias) get the epilogue of 0 without the sums.  A shape whose window exceeds
+// NARROW_LDS_FLOATS takes the generic kernel below; PTK_NARROW=0 forces it everywhere.
+#define NARROW_THREADS 256
+#define NARROW_LDS_FLOATS 16384
+
+__global__ void __launch_bounds__(NARROW_THREADS) conv_narrow_kernel(
+    const float *__restrict__ x, long long ldx, long long bsx, long long lim, int cin,
+    const float *__restrict__ wp, const float *__restrict__ bias, int cout, int K, int st, int dil,
+    int shift, float *__restrict__ y, long long ldy, long long bsy, long long n, int win, int epi0,
+    float a0, int epi1, float a1) {
+  extern __shared__ float xs[];   // [cin][win]; column 0 = input column t0 * st - shift
+  const int tid = threadIdx.x, b = blockIdx.y;
+  const long long t0 = (long long) blockIdx.x * NARROW_THREADS;
+  const long long c0 = t0 * st - shift;
+  const float *xb = x + (long long) b * bsx;
+  for (int i = tid; i < cin * win; i += NARROW_THREADS) {
+    const int ci = i / win, col = i - ci * win;
+    const long long c = c0 + col;
+    xs[i] = (c >= 0 && c < lim) ? xb[(long long) ci * ldx + c] : 0.0f;
+  }
+  __syncthreads();
+  const long long t = t0 + tid;
+  if (t >= n) return;
+  const int c4 = (cout + 3) & ~3;
+  float *yb = y + (long long) b * bsy + t;
+  const ptk_epi e0 = {epi0, a0, nullptr, 0, 0}, e1 = {epi1, a1, nullptr, 0, 0};
+  for (int m = 0; m < c4; m++) {
+    float v = (bias != nullptr && m < cout) ? bias[m] : 0.0f;
+    if (m < cout) {
+      const float *wq = wp + (long long) (m >> 2) * K * cin * 4 + (m & 3);
+      for (int k = 0; k < K; k++) {
+        const long long c = t * st + (long long) k * dil - shift;
+        if (c < 0 || c >= lim) continue;
+        const float *xk = xs + (tid * st + k * dil);
+        const float *wk = wq + (long long) k * cin * 4;
+        for (int ci = 0; ci < cin; ci++) v += wk[ci * 4] * xk[ci * win];
+      }
+    }
+    if (epi0) v = epi_apply(v, e0, b, m, t);
+    if (epi1) v = epi_apply(v, e1, b, m, t);
+    yb[(long long) m * ldy] = v;
+  }
+}
+
+// Thread tid of workgroup bx takes the delay-line step q = qlo + bx * NARROW_THREADS + tid and its
+// s outputs oi = q * s + r - pad (r < s) that fall in [0, Lout); the window holds input columns
+// [q0 - ntap + 1, q0 + NARROW_THREADS) of the workgroup's first step q0.
+__global__ void __launch_bounds__(NARROW_THREADS) convT_narrow_kernel(
+    const float *__restrict__ x, long long ldx, long long bsx, long long tin, int cin,
+    const float *__restrict__ wp, const float *__restrict__ bias, int cout, int s, int pad,
+    int ntap, float *__restrict__ y, long long ldy, long long bsy, long long Lout, long long qlo,
+    long long nq, int win) {
+  extern __shared__ float xs[];   // [cin][win]
+  const int tid = threadIdx.x, b = blockIdx.y;
+  const long long q0 = qlo + (long long) blockIdx.x * NARROW_THREADS;
+  const long long c0 = q0 - ntap + 1;
+  const float *xb = x + (long long) b * bsx;
+  for (int i = tid; i < cin * win; i += NARROW_THREADS) {
+    const int ci = i / win, col = i - ci * win;
+    const long long c = c0 + col;
+    xs[i] = (c >= 0 && c < tin) ? xb[(long long) ci * ldx + c] : 0.0f;
+  }
+  __syncthreads();
+  const long long q = q0 + tid;
+  if (q - qlo >= nq) return;
+  const int c4 = (cout + 3) & ~3;
+  float *yb = y + (long long) b * bsy;
+  for (int co = 0; co < c4; co++) {
+    for (int r = 0; r < s; r++) {
+      const long long oi = q * s + r - pad;
+      if (oi < 0 || oi >= Lout) continue;
+      float v = (bias != nullptr && co < cout) ? bias[co] : 0.0f;
+      if (co < cout) {
+        const int row = r * c4 + co;
+        const float *wq = wp + (long long) (row >> 2) * ntap * cin * 4 + (row & 3);
+        for (int j = 0; j < ntap; j++) {
+          const long long c = q - j;
+          if (c < 0 || c >= tin) continue;
+          const float *xj = xs + (tid + ntap - 1 - j);
+          const float *wj = wq + (long long) j * cin * 4;
+          for (int ci = 0; ci < cin; ci++) v += wj[ci * 4] * xj[ci * win];
+        }
+      }
+      yb[(long long) co * ldy + oi] = v;
+    }
+  }
+}
+
 __global__ void conv_simt_kernel(const float *__restrict__ x, long long ldx, long long bsx,
                                  long long lim, int cin, const float *__restrict__ wp,
                                  const float *__restrict__ bias, int cout, int K, int st, int dil,
@@ -1375,6 +1514,17 @@ extern "C" int ptk_conv_simt(const float *x, int64_t ldx, int64_t bsx, int64_t l
                              int dil, int shift, float *y, int64_t ldy, int64_t bsy, int64_t n,
                              int batch, int epi0, float a0, int epi1, float a1, void *s) {
   if (n <= 0 || batch <= 0) return 0;
+  const long long win = (long long) (NARROW_THREADS - 1) * stride + (long long) (K - 1) * dil + 1;
+  if (knob(KN_NARROW) && dil >= 1 && stride >= 1 && (long long) cin * win <= NARROW_LDS_FLOATS) {
+    dim3 grid((unsigned) ((n + NARROW_THREADS - 1) / NARROW_THREADS), (unsigned) batch);
+    hipLaunchKernelGGL(conv_narrow_kernel, grid, dim3(NARROW_THREADS),
+                       (size_t) cin * win * sizeof(float), (hipStream_t) s, x, (long long) ldx,
+                       (long long) bsx, (long long) lim, cin, wp, bias, cout, K, stride, dil, shift,
+                       y, (long long) ldy, (long long) bsy, (long long) n, (int) win, epi0, a0,
+                       epi1, a1);
+    HCHK(hipGetLastError());
+    return 0;
+  }
   const int c4 = (cout + 3) / 4 * 4;
   dim3 grid((unsigned) ((n + 255) / 256), (unsigned) c4, (unsigned) batch);
   hipLaunchKernelGGL(conv_simt_kernel, grid, dim3(256), 0, (hipStream_t) s, x, (long long) ldx,
@@ -1414,6 +1564,18 @@ extern "C" int ptk_convT_simt(const float *x, int64_t ldx, int64_t bsx, int64_t 
   if (Lout <= 0 || batch <= 0) return 0;
   const int c4 = (cout + 3) / 4 * 4;
   const int ntap = (K + st - 1) / st;
+  const long long win = NARROW_THREADS + ntap - 1;
+  if (knob(KN_NARROW) && st >= 1 && pad >= 0 && (long long) cin * win <= NARROW_LDS_FLOATS) {
+    // delay-line steps with an output in [0, Lout): u = oi + pad = q * st + r
+    const long long qlo = pad / st, nq = (Lout - 1 + pad) / st - qlo + 1;
+    dim3 grid((unsigned) ((nq + NARROW_THREADS - 1) / NARROW_THREADS), (unsigned) batch);
+    hipLaunchKernelGGL(convT_narrow_kernel, grid, dim3(NARROW_THREADS),
+                       (size_t) cin * win * sizeof(float), (hipStream_t) s, x, (long long) ldx,
+                       (long long) bsx, (long long) tin, cin, wp, bias, cout, st, pad, ntap, y,
+                       (long long) ldy, (long long) bsy, (long long) Lout, qlo, nq, (int) win);
+    HCHK(hipGetLastError());
+    return 0;
+  }
   dim3 grid((unsigned) ((Lout + 255) / 256), (unsigned) c4, (unsigned) batch);
   hipLaunchKernelGGL(convT_simt_kernel, grid, dim3(256), 0, (hipStream_t) s, x, (long long) ldx,
                      (long long) bsx, (long long) tin, cin, wp, bias, cout, st, pad, ntap, y,
@@ -1827,7 +1989,7 @@ static int launch_tail(int batch, const float *p, int64_t ldp, int64_t bsp, int6
   long long grid = grid_knob > 0 ? grid_knob : (grid_knob < 0 || resident <= 0 ? ntiles : resident);
   if (grid > ntiles) grid = ntiles;
   // looping workgroups split the tiles into one contiguous run per XCD (PTK_TAIL_XCD=0: no split)
-  const int xcd_run = grid < ntiles && grid % 8 == 0 && env_knob_or("PTK_TAIL_XCD", 1)
+  const int xcd_run = grid < ntiles && grid % 8 == 0 && knob(KN_TAIL_XCD)
       ? (int) ((ntiles + 7) / 8) : 0;
   const int stride = xcd_run ? (int) (grid / 8) : (int) grid;
   auto clamp = [nout](int64_t v) { return (int) (v < 0 ? 0 : (v > nout ? nout : v)); };
@@ -1857,11 +2019,11 @@ extern "C" int ptk_tail_batched(const float *p, int64_t ldp, int64_t bsp, int64_
   const ptk_emit all = {0, 0, nout, nout};
   const ptk_emit em = emit ? *emit : all;
   // Tile size: PTK_TAIL_OUT=256 / 512 / 1024 forces one.
-  const int knob = env_knob("PTK_TAIL_OUT"), gknob = env_knob("PTK_TAIL_GRID");
+  const int oknob = knob(KN_TAIL_OUT), gknob = knob(KN_TAIL_GRID);
   const long long t1k = (nout + 1023) / 1024 * batch, t512 = (nout + 511) / 512 * batch;
   hipStream_t st = (hipStream_t) s;
-  const int tout = knob == 256 || knob == 512 || knob == 1024
-      ? knob : (t1k >= 256 ? 1024 : (t512 >= 256 ? 512 : 256));
+  const int tout = oknob == 256 || oknob == 512 || oknob == 1024
+      ? oknob : (t1k >= 256 ? 1024 : (t512 >= 256 ? 512 : 256));
   if (tout == 1024)
     return launch_tail<1024>(batch, p, ldp, bsp, L, wav, bsw, consts, &em, gknob, st);
   if (tout == 512)

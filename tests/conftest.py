@@ -28,3 +28,32 @@ def pytest_configure(config):
 @pytest.fixture(scope="session")
 def pkg():
     return load_package()
+
+
+class KnobEnv:
+    """monkeypatch's setenv / delenv for the library's tuning knobs (PTK_CONV_*, PTK_TAIL_*,
+    PTD_WINDOW_*), which the library reads once per process: each change is followed by
+    ptd_debug_reload_env, so the next call sees it."""
+
+    def __init__(self, mp):
+        self._mp = mp
+
+    @staticmethod
+    def reload():
+        load_package().load().ptd_debug_reload_env()
+
+    def setenv(self, name, value):
+        self._mp.setenv(name, value)
+        self.reload()
+
+    def delenv(self, name, raising=True):
+        self._mp.delenv(name, raising=raising)
+        self.reload()
+
+
+@pytest.fixture
+def knob_env(monkeypatch):
+    """Knob changes for one test; the environment is restored and re-read when it ends."""
+    yield KnobEnv(monkeypatch)
+    monkeypatch.undo()
+    KnobEnv.reload()

@@ -4,7 +4,11 @@ LeakyReLU after conv_pre and each c1 as epilogue code 1, host glue in numpy), th
 reference's graph interpreter drives the library.  Its conv_post output must meet the per-layer
 bar against the oracle's decoder (which runs the reference's own CPU conv loops over the same
 graph) and against the device-resident decoder, and the waveform the tail makes of it the
-end-to-end bar."""
+end-to-end bar.  The interpreter's chained mode (c1 -> c2 kept on the device through conv_keep /
+conv_in_dev) and its PT_V21_DEVADD residency (residual adds, LeakyReLUs and branch sums through
+pt_v21_devadd_run / pt_v21_devleaky_run on device buffers) give the same bits as the per-call
+mode: the same kernels sum in the same order, and the device Add and LeakyReLU are the same fp32
+operations as the host's."""
 from __future__ import annotations
 
 import sys
@@ -77,3 +81,21 @@ def test_abi_decoder_vs_device_decoder_T226(env):
     pd = abi_decoder.device_conv_post(pkg, ctx, model, z)
     assert relerr(p, pd) < TOL
     assert np.array_equal(run.request(z), p)
+
+
+@pytest.mark.parametrize("mode", ["chained", "resident"])
+def test_abi_decoder_modes_match_per_call(env, mode):
+    ctx, model, ws, bs, run = env
+    say(f"ABI-driven decoder, {mode} mode, vs per-call mode")
+    other = abi_decoder.AbiDecoder(pkg, ctx, ws, bs, mode=mode)
+    try:
+        for T in (40, 226):
+            z = synth.latent(T, 700 + T)
+            ref = run.request(z)
+            c0 = list(other.calls)
+            got = other.request(z)
+            assert [other.calls[0] - c0[0], other.calls[1] - c0[1]] == [38, 2]
+            assert np.array_equal(got, ref), f"T={T}"
+            assert np.array_equal(other.request(z), ref), f"T={T} repeated"
+    finally:
+        other.close()

@@ -207,7 +207,7 @@ def test_tail_large_phase_logits_vs_oracle(env, scale):
 
 
 @pytest.mark.parametrize("L,batch", [(2, 1), (65, 3), (3617, 2)])
-def test_tail_block_size_gives_the_same_samples(env, L, batch, monkeypatch):
+def test_tail_block_size_gives_the_same_samples(env, L, batch, knob_env):
     """The tail kernel's tile size (256, 512 or 1024 samples, chosen from the work; forced here
     through PTK_TAIL_OUT) and its grid (a workgroup per tile, or fewer workgroups looping over the
     tiles, split into one run per XCD when the grid is a multiple of 8: PTK_TAIL_GRID) only change
@@ -221,13 +221,13 @@ def test_tail_block_size_gives_the_same_samples(env, L, batch, monkeypatch):
     outs = []
     for size, grid in (("256", "-1"), ("512", "-1"), ("1024", "-1"), ("256", "3"), ("1024", "2"),
                        ("512", "0"), ("256", "8"), ("512", "16")):
-        monkeypatch.setenv("PTK_TAIL_OUT", size)
-        monkeypatch.setenv("PTK_TAIL_GRID", grid)
+        knob_env.setenv("PTK_TAIL_OUT", size)
+        knob_env.setenv("PTK_TAIL_GRID", grid)
         dw.upload(ctx, np.full(batch * 16 * (L - 1), np.nan, np.float32))
         assert ctx.lib.ptd_tail(ctx.ptr, model.ptr, dp.ptr, L, batch, dw.ptr) == 0
         outs.append(dw.download(ctx).reshape(batch, 16 * (L - 1)))
-    monkeypatch.delenv("PTK_TAIL_OUT")
-    monkeypatch.delenv("PTK_TAIL_GRID")
+    knob_env.delenv("PTK_TAIL_OUT")
+    knob_env.delenv("PTK_TAIL_GRID")
     for o in outs[1:]:
         assert np.array_equal(outs[0], o)
     for i in range(batch):
@@ -277,7 +277,7 @@ LAYER_COLS = [(0, 150, 20, 70, 13, 31), (1, 60, 9, 33, 5, 17), (20, 90, 30, 41, 
 
 
 @pytest.mark.parametrize("rb,split", [(0, 0), (16, 1), (32, 2), (32, 4), (16, 4), (16, 8), (32, 8)])
-def test_layer_cols_per_item(env, rb, split, monkeypatch):
+def test_layer_cols_per_item(env, rb, split, knob_env):
     """A launch over part of the columns (the windowed decode's form: middle items [q0, q0 + nq),
     item 0 from ext_l earlier, the last item to ext_r later, tile shape of the full width) writes
     exactly those columns of each item, bit-identical to the full launch, and nothing else: conv
@@ -286,8 +286,8 @@ def test_layer_cols_per_item(env, rb, split, monkeypatch):
     ctx, model, ws, bs = env
     say(f"layer columns rb={rb} split={split}")
     if rb:
-        monkeypatch.setenv("PTK_CONV_RB", str(rb))
-        monkeypatch.setenv("PTK_CONV_SPLIT", str(split))
+        knob_env.setenv("PTK_CONV_RB", str(rb))
+        knob_env.setenv("PTK_CONV_SPLIT", str(split))
     lib = ctx.lib
     rng = np.random.default_rng(rb * 10 + split)
     for layer, T, off, nq, el, er in LAYER_COLS:
@@ -321,7 +321,7 @@ def test_layer_cols_per_item(env, rb, split, monkeypatch):
 
 @pytest.mark.parametrize("rb,split", [(16, 1), (16, 2), (16, 4), (16, 8), (32, 1), (32, 2), (32, 4),
                                       (32, 8)])
-def test_tile_shapes_vs_oracle(env, rb, split, monkeypatch):
+def test_tile_shapes_vs_oracle(env, rb, split, knob_env):
     """Every tile shape the launcher can pick (16- or 32-row tiles, channel split 1 / 2 / 4, and 8
     on the single-problem launches; forced through PTK_CONV_RB / PTK_CONV_SPLIT) against the
     oracle: a conv with a LeakyReLU epilogue,
@@ -330,8 +330,8 @@ def test_tile_shapes_vs_oracle(env, rb, split, monkeypatch):
     whole decode."""
     ctx, model, ws, bs = env
     say(f"tile shape rb={rb} split={split}")
-    monkeypatch.setenv("PTK_CONV_RB", str(rb))
-    monkeypatch.setenv("PTK_CONV_SPLIT", str(split))
+    knob_env.setenv("PTK_CONV_RB", str(rb))
+    knob_env.setenv("PTK_CONV_SPLIT", str(split))
     rng = np.random.default_rng(40 + rb + split)
     cases = [(0, 226, 0.0, 0.1), (1, 61, 0.1, 0.0), (20, 97, 0.1, 0.0), (39, 203, 0.0, 0.0)]
     for layer, T, in_a, epi_a in cases:
@@ -447,7 +447,7 @@ def test_config5_longform_windows_vs_full(env):
 
 
 @pytest.mark.parametrize("T,win,cx", [(1500, 96, 16), (777, 96, 16), (400, 48, 16)])
-def test_window_columns_change_no_sample(env, T, win, cx, monkeypatch):
+def test_window_columns_change_no_sample(env, T, win, cx, knob_env):
     """The windowed decode computes only the columns its kept samples depend on: with the arena
     poisoned (every column it leaves out reads NaN) its output is bit-identical to the same decode
     computing every column (PTD_WINDOW_CONE=0), at config 5's long-form shape and two others."""
@@ -456,10 +456,10 @@ def test_window_columns_change_no_sample(env, T, win, cx, monkeypatch):
     lib = ctx.lib
     z = synth.latent(T, 900 + T)
     dz, dw = dev_of(ctx, z), pkg.DevBuf(256 * T)
-    monkeypatch.setenv("PTD_WINDOW_CONE", "0")
+    knob_env.setenv("PTD_WINDOW_CONE", "0")
     assert lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, win, cx, dw.ptr) == 0
     whole = dw.download(ctx)
-    monkeypatch.delenv("PTD_WINDOW_CONE")
+    knob_env.delenv("PTD_WINDOW_CONE")
     dw.upload(ctx, np.full(256 * T, np.nan, np.float32))
     assert lib.ptd_debug_fill_arena(ctx.ptr, 0xFF) == 0
     assert lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, win, cx, dw.ptr) == 0
@@ -471,7 +471,7 @@ def test_window_columns_change_no_sample(env, T, win, cx, monkeypatch):
 
 @pytest.mark.parametrize("tout,grid", [("256", "7"), ("1024", "3"), ("512", "-1"), ("256", "8"),
                                        ("1024", "24")])
-def test_window_tail_tiles_and_grid_change_no_sample(env, tout, grid, monkeypatch):
+def test_window_tail_tiles_and_grid_change_no_sample(env, tout, grid, knob_env):
     """A windowed decode's tail skips the tiles with no kept samples: with a few workgroups looping
     over the tiles (PTK_TAIL_GRID), or one per tile, at every tile size, the long-form request
     (T = 1500 in 96/16 windows) is bit-identical to the default launch, and every sample is
@@ -484,20 +484,20 @@ def test_window_tail_tiles_and_grid_change_no_sample(env, tout, grid, monkeypatc
     dz, dw = dev_of(ctx, z), pkg.DevBuf(256 * T)
     assert lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, 96, 16, dw.ptr) == 0
     ref = dw.download(ctx)
-    monkeypatch.setenv("PTK_TAIL_OUT", tout)
-    monkeypatch.setenv("PTK_TAIL_GRID", grid)
+    knob_env.setenv("PTK_TAIL_OUT", tout)
+    knob_env.setenv("PTK_TAIL_GRID", grid)
     dw.upload(ctx, np.full(256 * T, np.nan, np.float32))
     assert lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, 96, 16, dw.ptr) == 0
     wav = dw.download(ctx)
-    monkeypatch.delenv("PTK_TAIL_OUT")
-    monkeypatch.delenv("PTK_TAIL_GRID")
+    knob_env.delenv("PTK_TAIL_OUT")
+    knob_env.delenv("PTK_TAIL_GRID")
     assert np.all(np.isfinite(wav))
     assert np.array_equal(wav, ref)
     dz.free(); dw.free()
 
 
 @pytest.mark.parametrize("T,mode", [(1500, "default"), (300, "2"), (1500, "2"), (600, "default")])
-def test_window_streams_change_no_sample(env, T, mode, monkeypatch):
+def test_window_streams_change_no_sample(env, T, mode, knob_env):
     """A batched run of windows split over the context's stream and a second stream (the default
     for runs of 16 windows or more; PTD_WINDOW_STREAMS=2 splits any run of two, =1 none) gives the
     same samples as the unsplit run, bit for bit, with the context's arena poisoned first; and a
@@ -510,15 +510,15 @@ def test_window_streams_change_no_sample(env, T, mode, monkeypatch):
     z2 = synth.latent(150, 7200)
     dz, dw = dev_of(ctx, z), pkg.DevBuf(256 * T)
     dz2, dw2 = dev_of(ctx, z2), pkg.DevBuf(256 * 150)
-    monkeypatch.setenv("PTD_WINDOW_STREAMS", "1")
+    knob_env.setenv("PTD_WINDOW_STREAMS", "1")
     assert lib.ptd_decode_windows(ctx.ptr, model.ptr, dz.ptr, T, 96, 16, dw.ptr) == 0
     ref = dw.download(ctx)
     assert lib.ptd_decode(ctx.ptr, model.ptr, dz2.ptr, 150, 1, dw2.ptr) == 0
     ref2 = dw2.download(ctx)
     if mode == "default":
-        monkeypatch.delenv("PTD_WINDOW_STREAMS")
+        knob_env.delenv("PTD_WINDOW_STREAMS")
     else:
-        monkeypatch.setenv("PTD_WINDOW_STREAMS", mode)
+        knob_env.setenv("PTD_WINDOW_STREAMS", mode)
     for rep in range(2):
         dw.upload(ctx, np.full(256 * T, np.nan, np.float32))
         dw2.upload(ctx, np.full(256 * 150, np.nan, np.float32))
@@ -531,7 +531,7 @@ def test_window_streams_change_no_sample(env, T, mode, monkeypatch):
         b.free()
 
 
-def test_window_split_falls_back_to_one_stream_in_a_small_arena(env, monkeypatch):
+def test_window_split_falls_back_to_one_stream_in_a_small_arena(env, knob_env):
     """A context whose arena holds the unsplit batched run (22 windows of the T = 1500 request) but
     not both halves of the split at once keeps the run on its own stream: the decode succeeds and
     matches the split decode of a roomy context bit for bit."""

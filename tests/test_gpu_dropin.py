@@ -144,22 +144,30 @@ def test_reference_stream_driver_through_the_library(model, tmp_path, win, cx):
     """The reference's overlap-save streaming path (`--stream WIN CTX`: pt_v21_stream_open runs
     the encoder once, then pt_v21_stream_chunk the decoder's convs and convTs on each window,
     main_v21.c:331-370, pt_v21_host.c:2789-2902) with the library as its device: the stitched
-    waveform against what the reference's CPU build stitched on the same 97-token case
-    (tests/golden/ref_decoder_ckpt_T198.npz, written by tests/golden/gen_decoder_ckpt.py on the
-    same container and case), >= 60 dB and closer to it than to the full decode."""
+    waveform against what the reference's CPU build stitched on the same case (for the 97-token
+    case the committed tests/golden/ref_decoder_ckpt_T198.npz, written by
+    tests/golden/gen_decoder_ckpt.py on the same container and case; for the 40-token case the CPU
+    build run here in stream mode), >= 60 dB and closer to it than to the full decode."""
     d, case, cpu_wav = model
     g = np.load(STREAM_FIXTURE)
-    if int(np.load(case / "x_lengths.npy")[0]) != int(g["n_tokens"]):
-        pytest.skip("the streamed fixture is the 97-token case")
+    full = np.load(cpu_wav).ravel()
+    if int(np.load(case / "x_lengths.npy")[0]) == int(g["n_tokens"]):
+        assert np.array_equal(full, g["wav"])   # the same container and case as the fixture
+        ref = g[f"stream_{win}_{cx}"]
+    else:
+        say(f"reference CPU build --stream {win} {cx}")
+        rc = _run([CPU_BIN, "--cpu", "--container", d / "model.ptk", "--case", case, "--out",
+                   tmp_path / "cpu_s.npy", "--stream", win, cx], 600)
+        assert (tmp_path / "cpu_s.npy").exists(), rc.stdout[-2000:] + rc.stderr[-2000:]
+        ref = np.load(tmp_path / "cpu_s.npy").ravel()
     say(f"reference driver --stream {win} {cx} through the library")
     r = _run([DEV_BIN, "--container", d / "model.ptk", "--case", case, "--out", tmp_path / "s.npy",
               "--stream", win, cx], 300)
-    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    # (its exit code is its gate against the full decode, which a stream need not pass)
+    assert (tmp_path / "s.npy").exists() and f"win={win} ctx={cx}" in r.stderr, \
+        r.stdout[-2000:] + r.stderr[-2000:]
     got = np.load(tmp_path / "s.npy").ravel()
-    full = np.load(cpu_wav).ravel()
-    assert np.array_equal(full, g["wav"])   # the same container and case as the fixture
-    ref = g[f"stream_{win}_{cx}"]
-    assert got.shape == ref.shape
+    assert got.shape == ref.shape == full.shape
     s_stream, s_full = np_ref.sndr(got, ref), np_ref.sndr(got, full)
     say(f"stream {win}/{cx}: {s_stream:.1f} dB vs the CPU build's stream, {s_full:.1f} dB vs its full decode")
     assert s_stream >= 60.0 and s_stream >= s_full + 20.0
@@ -169,11 +177,17 @@ def test_reference_stream_driver_through_the_library(model, tmp_path, win, cx):
 
 @pytest.mark.skipif(not PAR_BIN.exists(), reason="oracle/_ref/pt_v21_par_mi355x not built")
 @pytest.mark.parametrize("wait", [{}, {"PT_V21_WAIT_US": "200"},
-                                  {"PT_V21_WAIT_US": "200", "PT_V21_WAIT_ADAPT": "0"}],
-                         ids=["runtime-wait", "sleep-poll-200us", "sleep-poll-always"])
+                                  {"PT_V21_WAIT_US": "200", "PT_V21_WAIT_ADAPT": "0"},
+                                  {"PT_V21_SYNC": "0"}, {"PT_V21_SYNC": "1"},
+                                  {"PT_V21_UP_PAR": "0"}],
+                         ids=["runtime-wait", "sleep-poll-200us", "sleep-poll-always",
+                              "sync-spin", "sync-blocking", "upload-serialised"])
 def test_reference_multistream_driver(model, wait):
     """8 concurrent streams under the driver's own gate, with the runtime's stream wait and with
-    the reference's sleep-poll wait policy (its default 200 us, adaptive or always sleeping)."""
+    the reference's sleep-poll wait policy (its default 200 us, adaptive or always sleeping), with
+    its host-wait scheduling modes (PT_V21_SYNC 0 spin, 1 blocking), and with the weight upload
+    serialised under the pool lock (PT_V21_UP_PAR=0: the first context copies every record, the
+    other seven find them resident)."""
     d, case, _ = model
     say("reference multi-stream driver, 8 streams")
     rp = _run([PAR_BIN, "--container", d / "model.ptk", "--case", case, "--parallel", 8], 300, wait)

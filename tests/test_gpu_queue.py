@@ -214,7 +214,7 @@ def test_queue_staggered_submissions(env):
 
 @pytest.mark.parametrize("parts_env", [("PTD_WINDOW_PARTS", "4"), ("PTD_WINDOW_STREAMS", "1"),
                                        ("PTD_WINDOW_STREAMS", "2")])
-def test_queue_window_split_beyond_prepared_streams(env, parts_env, monkeypatch):
+def test_queue_window_split_beyond_prepared_streams(env, parts_env, knob_env):
     """The queue makes each worker's extra stream for the default two-part split when it is
     created.  A split in four parts asked for afterwards makes the two more streams it needs on
     first use. Keeping every run on one stream, or splitting every run in two, works on the same
@@ -223,15 +223,15 @@ def test_queue_window_split_beyond_prepared_streams(env, parts_env, monkeypatch)
     lib = ctx.lib
     T, seed, wf, w, cx = 2600, 77, 48, 96, 16   # 39 full windows: four parts of at least 8
     say(f"queue: window split with {parts_env[0]}={parts_env[1]} after the queue is made")
-    monkeypatch.delenv("PTD_WINDOW_PARTS", raising=False)
-    monkeypatch.delenv("PTD_WINDOW_STREAMS", raising=False)
+    knob_env.delenv("PTD_WINDOW_PARTS", raising=False)
+    knob_env.delenv("PTD_WINDOW_STREAMS", raising=False)
     arena = int(lib.ptd_windows2_arena_bytes(T, wf, w, cx)) + (16 << 20)
-    monkeypatch.setenv("PTD_WINDOW_STREAMS", "1")
+    knob_env.setenv("PTD_WINDOW_STREAMS", "1")
     ref = _expected(ctx, model, (T, seed, wf, w, cx, 0.0))
-    monkeypatch.delenv("PTD_WINDOW_STREAMS")
+    knob_env.delenv("PTD_WINDOW_STREAMS")
     q = lib.ptd_queue_create(model.ptr, 2, arena, 8)
     assert q
-    monkeypatch.setenv(*parts_env)
+    knob_env.setenv(*parts_env)
     bufs, jobs = _jobs(ctx, [(T, seed, wf, w, cx, 0.0), (T, seed, wf, w, cx, 1.0)])
     try:
         ids = [lib.ptd_queue_submit(q, C.byref(j)) for j in jobs]
