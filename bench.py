@@ -315,16 +315,6 @@ NARROW_FIR = dict(cin=4, T=57856 + 62, K=63, cout=1)
 NARROW_OLA = dict(batch=4, cin=16, tin=3617, K=16, s=4, cout=1)
 
 
-def narrow_bytes():
-    """Algorithmic HBM bytes of one launch (inputs, weights, the cout4 output rows)."""
-    f, o = NARROW_FIR, NARROW_OLA
-    fir = 4.0 * (f["cin"] * f["T"] + 4 * f["K"] * f["cin"] + 4 * (f["T"] - f["K"] + 1))
-    lout = (o["tin"] - 1) * o["s"] + o["K"]
-    ola = 4.0 * (o["batch"] * o["cin"] * o["tin"] + o["s"] * 4 * (o["K"] // o["s"]) * o["cin"]
-                 + o["batch"] * 4 * lout)
-    return fir, ola
-
-
 def narrow_abi_loop(pkg, lib, ctx, n):
     """n pt_v21_conv calls at the PQMF FIR's shape and n pt_v21_convT calls at the iSTFT
     overlap-add's, on host buffers (each call copies, launches the narrow kernel and waits), for a

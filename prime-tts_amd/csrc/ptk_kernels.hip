@@ -1390,98 +1390,202 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
 // Narrow problems (the cout = 1..15 convs of the tail, 1-channel inputs): one thread per output,
 // summing over tap then channel onto the bias in the reference's order.
 // ------------------------------------------------------------------------------ narrow convs
-// Convs and convTs with few output rows on the reference ABI path (cout4 < 16: the PQMF synthesis
-// FIR 4 -> 1 K 63; the iSTFT overlap-add 16 -> 1 and window sum 1 -> 1, K 16 s 4; the PQMF x4
-// zero-insert 4 -> 4 K 4 s 4).  A workgroup of NARROW_THREADS threads takes that many consecutive
-// output columns (convT: delay-line steps q, each giving s outputs) of one batch item, stages the
-// input window they read, [cin][win], in LDS once, and each thread computes its column for every
-// real output row.  The weights are read with uniform addresses (scalar loads).  The order per
-// output is the generic kernels' (bias, tap ascending, channel ascending, out-of-range columns
-// skipped), so the results are the same bits.  The layout's padding rows (cout..cout4-1, zero
-// weights and bias) get the epilogue of 0 without the sums.  A shape whose window exceeds
-// NARROW_LDS_FLOATS takes the generic kernel below; PTK_NARROW=0 forces it everywhere.
+// Convs and convTs with few output rows on the reference ABI path (cout4 < 16, channel counts 1,
+// 4 or 16: the PQMF synthesis FIR 4 -> 1 K 63; the iSTFT overlap-add 16 -> 1 and window sum
+// 1 -> 1, K 16 s 4; the PQMF x4 zero-insert 4 -> 4 K 4 s 4).  A workgroup stages in LDS, once,
+// the input window its outputs read, as [column][CIN] (a column's channels in one to four 16-byte
+// reads; the column stride padded to CIN + 4 floats for CIN 16, so a wave's reads spread over all
+// banks), and the real rows' weights, [row][tap][CIN] (conv) or [row][tap][CIN][s] (convT).  Each
+// output is one chain of FMAs in the generic kernels' order (bias, tap ascending, channel
+// ascending, taps whose input column is outside the sequence skipped), so the results are the
+// same bits.  The chip is nearly empty at these sizes, so the work is spread over many waves: one
+// conv output per thread, its taps' operands read one tap ahead into two alternating register
+// sets; a convT step's s phases per thread, sharing each input value.  (A first form, a plain loop
+// with its reads waiting one at a time, took 14-38 us per launch; four conv outputs per thread
+// gave 228 waves each issuing ~4700 instructions one at a time: 19 us.)  The layout's padding rows
+// (cout..cout4-1, zero weights and bias) get the epilogue of 0 without the sums.  Other channel
+// counts, windows past NARROW_LDS_FLOATS and sizes past 2^31 take the generic kernels below;
+// PTK_NARROW=0 forces them everywhere.
 #define NARROW_THREADS 256
-#define NARROW_LDS_FLOATS 16384
+#define NARROW_LDS_FLOATS 12288   // 48 KB of dynamic LDS per workgroup
+#define NARROW_SMAX 4             // convT phases (stride) a thread keeps in registers
 
+// floats per staged window column
+template <int CIN>
+__host__ __device__ constexpr int narrow_cs() { return CIN >= 16 ? CIN + 4 : CIN; }
+
+// CIN consecutive floats from LDS (16-byte aligned when CIN % 4 == 0) into registers
+template <int CIN>
+__device__ __forceinline__ void lds_cols(float (&v)[CIN], const float *p) {
+  if constexpr (CIN % 4 == 0) {
+#pragma unroll
+    for (int q = 0; q < CIN / 4; q++) {
+      const float4 t = reinterpret_cast<const float4 *>(p)[q];
+      v[4 * q] = t.x;
+      v[4 * q + 1] = t.y;
+      v[4 * q + 2] = t.z;
+      v[4 * q + 3] = t.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < CIN; i++) v[i] = p[i];
+  }
+}
+
+// Stages columns [0, win) of rows [0, CIN) into xs[col][narrow_cs<CIN>] (column c0 + col of the
+// item, 0 outside [0, lim)).  A thread's columns col = tid + p * NARROW_THREADS are taken PG at a
+// time, and all PG * CIN loads of a group are issued before its stores, so the window costs about
+// one global load latency per group.
+template <int CIN>
+__device__ __forceinline__ void narrow_stage(float *__restrict__ xs, const float *__restrict__ xb,
+                                             long long ldx, int c0, int lim, int win, int tid) {
+  constexpr int PG = CIN >= 16 ? 2 : 16 / CIN, CS = narrow_cs<CIN>();
+  for (int col0 = tid; col0 < win; col0 += PG * NARROW_THREADS) {
+    float v[PG][CIN];
+#pragma unroll
+    for (int g = 0; g < PG; g++) {
+      const int c = c0 + col0 + g * NARROW_THREADS;
+      const bool ok = col0 + g * NARROW_THREADS < win && c >= 0 && c < lim;
+      const float *src = xb + (ok ? c : 0);
+#pragma unroll
+      for (int ci = 0; ci < CIN; ci++) v[g][ci] = ok ? src[(long long) ci * ldx] : 0.0f;
+    }
+#pragma unroll
+    for (int g = 0; g < PG; g++) {
+      const int col = col0 + g * NARROW_THREADS;
+      if (col >= win) break;
+      if constexpr (CIN % 4 == 0) {
+#pragma unroll
+        for (int q = 0; q < CIN / 4; q++)
+          reinterpret_cast<float4 *>(xs + col * CS)[q] =
+              make_float4(v[g][4 * q], v[g][4 * q + 1], v[g][4 * q + 2], v[g][4 * q + 3]);
+      } else {
+#pragma unroll
+        for (int ci = 0; ci < CIN; ci++) xs[col * CS + ci] = v[g][ci];
+      }
+    }
+  }
+}
+
+template <int CIN>
+__device__ __forceinline__ float narrow_fma(float acc, const float (&w)[CIN], const float (&x)[CIN]) {
+#pragma unroll
+  for (int ci = 0; ci < CIN; ci++) acc += w[ci] * x[ci];
+  return acc;
+}
+
+template <int CIN>
 __global__ void __launch_bounds__(NARROW_THREADS) conv_narrow_kernel(
-    const float *__restrict__ x, long long ldx, long long bsx, long long lim, int cin,
-    const float *__restrict__ wp, const float *__restrict__ bias, int cout, int K, int st, int dil,
-    int shift, float *__restrict__ y, long long ldy, long long bsy, long long n, int win, int epi0,
-    float a0, int epi1, float a1) {
-  extern __shared__ float xs[];   // [cin][win]; column 0 = input column t0 * st - shift
+    const float *__restrict__ x, long long ldx, long long bsx, int lim, const float *__restrict__ wp,
+    const float *__restrict__ bias, int cout, int K, int st, int dil, int shift,
+    float *__restrict__ y, long long ldy, long long bsy, int n, int win, int epi0, float a0,
+    int epi1, float a1) {
+  constexpr int CS = narrow_cs<CIN>();
+  extern __shared__ float4 lds4[];
+  float *const xs = reinterpret_cast<float *>(lds4);   // [win][CS]; column 0 = input t0*st - shift
+  float *const ws = xs + ((win * CS + 3) & ~3);        // [cout][K][CIN]
   const int tid = threadIdx.x, b = blockIdx.y;
-  const long long t0 = (long long) blockIdx.x * NARROW_THREADS;
-  const long long c0 = t0 * st - shift;
-  const float *xb = x + (long long) b * bsx;
-  for (int i = tid; i < cin * win; i += NARROW_THREADS) {
-    const int ci = i / win, col = i - ci * win;
-    const long long c = c0 + col;
-    xs[i] = (c >= 0 && c < lim) ? xb[(long long) ci * ldx + c] : 0.0f;
+  const int t0 = blockIdx.x * NARROW_THREADS;
+  narrow_stage<CIN>(xs, x + (long long) b * bsx, ldx, t0 * st - shift, lim, win, tid);
+  for (int i = tid; i < cout * K * CIN; i += NARROW_THREADS) {
+    const int m = i / (K * CIN), r = i - m * (K * CIN), k = r / CIN, ci = r - k * CIN;
+    ws[i] = wp[((long long) (m >> 2) * K + k) * CIN * 4 + ci * 4 + (m & 3)];
   }
   __syncthreads();
-  const long long t = t0 + tid;
+  const int t = t0 + tid;
   if (t >= n) return;
+  // taps whose input column t * st + k * dil - shift lies in [0, lim): k in [klo, khi)
+  const int base = t * st - shift;
+  int klo = base >= 0 ? 0 : (-base + dil - 1) / dil;
+  int khi = base >= lim ? 0 : (lim - base + dil - 1) / dil;
+  khi = khi < K ? khi : K;
+  klo = klo < khi ? klo : khi;
   const int c4 = (cout + 3) & ~3;
-  float *yb = y + (long long) b * bsy + t;
   const ptk_epi e0 = {epi0, a0, nullptr, 0, 0}, e1 = {epi1, a1, nullptr, 0, 0};
+  const float *const xt = xs + tid * st * CS;
+  const int kstep = dil * CS;
   for (int m = 0; m < c4; m++) {
     float v = (bias != nullptr && m < cout) ? bias[m] : 0.0f;
-    if (m < cout) {
-      const float *wq = wp + (long long) (m >> 2) * K * cin * 4 + (m & 3);
-      for (int k = 0; k < K; k++) {
-        const long long c = t * st + (long long) k * dil - shift;
-        if (c < 0 || c >= lim) continue;
-        const float *xk = xs + (tid * st + k * dil);
-        const float *wk = wq + (long long) k * cin * 4;
-        for (int ci = 0; ci < cin; ci++) v += wk[ci * 4] * xk[ci * win];
+    if (m < cout && klo < khi) {
+      const float *const wm = ws + m * K * CIN;
+      // operands of the next tap read into the other register set while this tap's FMAs run;
+      // the read is unconditional (a tap past the last re-reads the last), so the wait before
+      // the FMAs leaves it in flight
+      const int klast = khi - 1;
+      float wa[CIN], xa[CIN], wb[CIN], xb2[CIN];
+      lds_cols<CIN>(wa, wm + klo * CIN);
+      lds_cols<CIN>(xa, xt + klo * kstep);
+      for (int k = klo;; k += 2) {
+        const int k1 = k + 1 < klast ? k + 1 : klast, k2 = k + 2 < klast ? k + 2 : klast;
+        lds_cols<CIN>(wb, wm + k1 * CIN);
+        lds_cols<CIN>(xb2, xt + k1 * kstep);
+        v = narrow_fma<CIN>(v, wa, xa);
+        if (k + 1 >= khi) break;
+        lds_cols<CIN>(wa, wm + k2 * CIN);
+        lds_cols<CIN>(xa, xt + k2 * kstep);
+        v = narrow_fma<CIN>(v, wb, xb2);
+        if (k + 2 >= khi) break;
       }
     }
     if (epi0) v = epi_apply(v, e0, b, m, t);
     if (epi1) v = epi_apply(v, e1, b, m, t);
-    yb[(long long) m * ldy] = v;
+    y[(long long) b * bsy + (long long) m * ldy + t] = v;
   }
 }
 
 // Thread tid of workgroup bx takes the delay-line step q = qlo + bx * NARROW_THREADS + tid and its
-// s outputs oi = q * s + r - pad (r < s) that fall in [0, Lout); the window holds input columns
+// s outputs oi = q * s + r - pad (r < s) that fall in [0, Lout), all s phases at once (s
+// independent sums over the same input values); the window holds input columns
 // [q0 - ntap + 1, q0 + NARROW_THREADS) of the workgroup's first step q0.
+template <int CIN>
 __global__ void __launch_bounds__(NARROW_THREADS) convT_narrow_kernel(
-    const float *__restrict__ x, long long ldx, long long bsx, long long tin, int cin,
-    const float *__restrict__ wp, const float *__restrict__ bias, int cout, int s, int pad,
-    int ntap, float *__restrict__ y, long long ldy, long long bsy, long long Lout, long long qlo,
-    long long nq, int win) {
-  extern __shared__ float xs[];   // [cin][win]
+    const float *__restrict__ x, long long ldx, long long bsx, int tin, const float *__restrict__ wp,
+    const float *__restrict__ bias, int cout, int s, int pad, int ntap, float *__restrict__ y,
+    long long ldy, long long bsy, int Lout, int qlo, int nq, int win) {
+  constexpr int CS = narrow_cs<CIN>();
+  extern __shared__ float4 lds4[];
+  float *const xs = reinterpret_cast<float *>(lds4);   // [win][CS]
+  float *const ws = xs + ((win * CS + 3) & ~3);        // [cout][ntap][CIN][NARROW_SMAX]
   const int tid = threadIdx.x, b = blockIdx.y;
-  const long long q0 = qlo + (long long) blockIdx.x * NARROW_THREADS;
-  const long long c0 = q0 - ntap + 1;
-  const float *xb = x + (long long) b * bsx;
-  for (int i = tid; i < cin * win; i += NARROW_THREADS) {
-    const int ci = i / win, col = i - ci * win;
-    const long long c = c0 + col;
-    xs[i] = (c >= 0 && c < tin) ? xb[(long long) ci * ldx + c] : 0.0f;
+  const int c4 = (cout + 3) & ~3;
+  const int q0 = qlo + blockIdx.x * NARROW_THREADS;
+  narrow_stage<CIN>(xs, x + (long long) b * bsx, ldx, q0 - ntap + 1, tin, win, tid);
+  for (int i = tid; i < cout * ntap * CIN * NARROW_SMAX; i += NARROW_THREADS) {
+    const int r = i % NARROW_SMAX, rest = i / NARROW_SMAX, ci = rest % CIN, rest2 = rest / CIN;
+    const int j = rest2 % ntap, co = rest2 / ntap, row = r * c4 + co;
+    ws[i] = r < s ? wp[((long long) (row >> 2) * ntap + j) * CIN * 4 + ci * 4 + (row & 3)] : 0.0f;
   }
   __syncthreads();
-  const long long q = q0 + tid;
+  const int q = q0 + tid;
   if (q - qlo >= nq) return;
-  const int c4 = (cout + 3) & ~3;
+  // taps whose input column q - j lies in [0, tin): j in [jlo, jhi)
+  const int jlo = q >= tin ? q - tin + 1 : 0;
+  const int jhi = q + 1 < ntap ? q + 1 : ntap;
   float *yb = y + (long long) b * bsy;
+  const float *const xq = xs + (tid + ntap - 1) * CS;   // input column q - j at xq[-j * CS]
   for (int co = 0; co < c4; co++) {
-    for (int r = 0; r < s; r++) {
-      const long long oi = q * s + r - pad;
-      if (oi < 0 || oi >= Lout) continue;
-      float v = (bias != nullptr && co < cout) ? bias[co] : 0.0f;
-      if (co < cout) {
-        const int row = r * c4 + co;
-        const float *wq = wp + (long long) (row >> 2) * ntap * cin * 4 + (row & 3);
-        for (int j = 0; j < ntap; j++) {
-          const long long c = q - j;
-          if (c < 0 || c >= tin) continue;
-          const float *xj = xs + (tid + ntap - 1 - j);
-          const float *wj = wq + (long long) j * cin * 4;
-          for (int ci = 0; ci < cin; ci++) v += wj[ci * 4] * xj[ci * win];
-        }
+    const float bv = (bias != nullptr && co < cout) ? bias[co] : 0.0f;
+    float acc[NARROW_SMAX];
+#pragma unroll
+    for (int r = 0; r < NARROW_SMAX; r++) acc[r] = bv;
+    if (co < cout) {
+      const float *const wc = ws + co * ntap * CIN * NARROW_SMAX;
+      for (int j = jlo; j < jhi; j++) {
+        // the tap's operands all read before its FMAs
+        float xv[CIN], w[CIN][NARROW_SMAX];
+        lds_cols<CIN>(xv, xq - j * CS);
+#pragma unroll
+        for (int ci = 0; ci < CIN; ci++) lds_cols<NARROW_SMAX>(w[ci], wc + (j * CIN + ci) * NARROW_SMAX);
+#pragma unroll
+        for (int ci = 0; ci < CIN; ci++)
+#pragma unroll
+          for (int r = 0; r < NARROW_SMAX; r++) acc[r] += w[ci][r] * xv[ci];
       }
-      yb[(long long) co * ldy + oi] = v;
+    }
+#pragma unroll
+    for (int r = 0; r < NARROW_SMAX; r++) {
+      const int oi = q * s + r - pad;
+      if (r < s && oi >= 0 && oi < Lout) yb[(long long) co * ldy + oi] = acc[r];
     }
   }
 }
@@ -1514,14 +1618,25 @@ extern "C" int ptk_conv_simt(const float *x, int64_t ldx, int64_t bsx, int64_t l
                              int dil, int shift, float *y, int64_t ldy, int64_t bsy, int64_t n,
                              int batch, int epi0, float a0, int epi1, float a1, void *s) {
   if (n <= 0 || batch <= 0) return 0;
-  const long long win = (long long) (NARROW_THREADS - 1) * stride + (long long) (K - 1) * dil + 1;
-  if (knob(KN_NARROW) && dil >= 1 && stride >= 1 && (long long) cin * win <= NARROW_LDS_FLOATS) {
-    dim3 grid((unsigned) ((n + NARROW_THREADS - 1) / NARROW_THREADS), (unsigned) batch);
-    hipLaunchKernelGGL(conv_narrow_kernel, grid, dim3(NARROW_THREADS),
-                       (size_t) cin * win * sizeof(float), (hipStream_t) s, x, (long long) ldx,
-                       (long long) bsx, (long long) lim, cin, wp, bias, cout, K, stride, dil, shift,
-                       y, (long long) ldy, (long long) bsy, (long long) n, (int) win, epi0, a0,
-                       epi1, a1);
+  const long long per_wg = NARROW_THREADS;
+  const long long win = (per_wg - 1) * stride + (long long) (K - 1) * dil + 1;
+  const long long cs = cin >= 16 ? cin + 4 : cin;
+  const long long lds_floats = ((cs * win + 3) & ~3LL) + (long long) cout * K * cin;
+  // 32-bit column arithmetic in the kernel: every window column, output and input index < 2^31
+  const bool small = lim < INT32_MAX && (n + per_wg) * stride + win + shift < INT32_MAX;
+  if (knob(KN_NARROW) && (cin == 1 || cin == 4 || cin == 16) && dil >= 1 && stride >= 1 && small &&
+      lds_floats <= NARROW_LDS_FLOATS) {
+    dim3 grid((unsigned) ((n + per_wg - 1) / per_wg), (unsigned) batch);
+    const size_t lds = (size_t) lds_floats * sizeof(float);
+#define NARROW_CONV_LAUNCH(CINV)                                                                  \
+  hipLaunchKernelGGL(conv_narrow_kernel<CINV>, grid, dim3(NARROW_THREADS), lds, (hipStream_t) s, x, \
+                     (long long) ldx, (long long) bsx, (int) lim, wp, bias, cout, K, stride, dil,  \
+                     shift, y, (long long) ldy, (long long) bsy, (int) n, (int) win, epi0, a0,     \
+                     epi1, a1)
+    if (cin == 1) NARROW_CONV_LAUNCH(1);
+    else if (cin == 4) NARROW_CONV_LAUNCH(4);
+    else NARROW_CONV_LAUNCH(16);
+#undef NARROW_CONV_LAUNCH
     HCHK(hipGetLastError());
     return 0;
   }
@@ -1565,14 +1680,23 @@ extern "C" int ptk_convT_simt(const float *x, int64_t ldx, int64_t bsx, int64_t 
   const int c4 = (cout + 3) / 4 * 4;
   const int ntap = (K + st - 1) / st;
   const long long win = NARROW_THREADS + ntap - 1;
-  if (knob(KN_NARROW) && st >= 1 && pad >= 0 && (long long) cin * win <= NARROW_LDS_FLOATS) {
+  const long long cs = cin >= 16 ? cin + 4 : cin;
+  const long long lds_floats = ((cs * win + 3) & ~3LL) + (long long) NARROW_SMAX * cout * ntap * cin;
+  const bool small = tin < INT32_MAX - NARROW_THREADS && Lout + pad + (long long) NARROW_THREADS * st < INT32_MAX;
+  if (knob(KN_NARROW) && (cin == 1 || cin == 4 || cin == 16) && st >= 1 && st <= NARROW_SMAX &&
+      pad >= 0 && small && lds_floats <= NARROW_LDS_FLOATS) {
     // delay-line steps with an output in [0, Lout): u = oi + pad = q * st + r
     const long long qlo = pad / st, nq = (Lout - 1 + pad) / st - qlo + 1;
     dim3 grid((unsigned) ((nq + NARROW_THREADS - 1) / NARROW_THREADS), (unsigned) batch);
-    hipLaunchKernelGGL(convT_narrow_kernel, grid, dim3(NARROW_THREADS),
-                       (size_t) cin * win * sizeof(float), (hipStream_t) s, x, (long long) ldx,
-                       (long long) bsx, (long long) tin, cin, wp, bias, cout, st, pad, ntap, y,
-                       (long long) ldy, (long long) bsy, (long long) Lout, qlo, nq, (int) win);
+    const size_t lds = (size_t) lds_floats * sizeof(float);
+#define NARROW_CONVT_LAUNCH(CINV)                                                                 \
+  hipLaunchKernelGGL(convT_narrow_kernel<CINV>, grid, dim3(NARROW_THREADS), lds, (hipStream_t) s, \
+                     x, (long long) ldx, (long long) bsx, (int) tin, wp, bias, cout, st, pad, ntap, \
+                     y, (long long) ldy, (long long) bsy, (int) Lout, (int) qlo, (int) nq, (int) win)
+    if (cin == 1) NARROW_CONVT_LAUNCH(1);
+    else if (cin == 4) NARROW_CONVT_LAUNCH(4);
+    else NARROW_CONVT_LAUNCH(16);
+#undef NARROW_CONVT_LAUNCH
     HCHK(hipGetLastError());
     return 0;
   }

@@ -437,3 +437,65 @@ def test_convT_random_vs_oracle(ctx, cfg):
     y = gpu_convT(ctx, x, wp, b, cout, K, s, pad)
     assert y.shape == ref.shape
     assert relerr(y, ref) < TOL
+
+
+# Narrow shapes the reference interpreter hands to the ABI (cout4 < 16), and variants:
+# (batch, cin, T, cout, K, stride, pad, dil, epi0, epi1, a0, a1, padded rows, bias)
+NARROW_CONV = [
+    (1, 4, 57856 + 62, 1, 63, 1, 0, 1, 0, 0, 0.0, 0.0, True, True),   # the PQMF synthesis FIR
+    (2, 3, 500, 6, 5, 2, 2, 3, 1, 4, 0.1, 0.25, False, True),          # stride, dilation, epilogues
+    (3, 8, 300, 12, 7, 1, 3, 1, 0, 0, 0.0, 0.0, False, False),         # batch, no bias
+    (1, 1, 1000, 4, 11, 1, 5, 2, 2, 3, 0.0, 1.5, False, True),         # cin 1, relu then scale
+    (1, 40, 700, 2, 9, 3, 4, 4, 0, 0, 0.0, 0.0, False, True),          # window past LDS: generic
+]
+# (batch, cin, tin, cout, K, stride, pad, bias)
+NARROW_CONVT = [
+    (4, 16, 3617, 1, 16, 4, 0, False),   # the iSTFT overlap-add
+    (4, 1, 3617, 1, 16, 4, 0, False),    # the window sum
+    (1, 4, 14464, 4, 4, 4, 0, False),    # the PQMF x4 zero-insert
+    (2, 5, 300, 3, 7, 3, 2, True),       # a partial last tap (K % s != 0), padding
+    (1, 70, 100, 8, 16, 4, 6, True),     # window past LDS: generic
+]
+
+
+@pytest.mark.parametrize("case", NARROW_CONV, ids=[f"conv{i}" for i in range(len(NARROW_CONV))])
+def test_narrow_conv_matches_generic_and_oracle(ctx, case, knob_env):
+    """The narrow conv kernel (input window staged in LDS, real rows only) gives the generic SIMT
+    kernel's bits (PTK_NARROW=0) on the narrow ABI shapes, and both meet the oracle bar."""
+    B, cin, T, cout, K, st, pad, dil, e0, e1, a0, a1, padded, with_bias = case
+    say(f"narrow conv {case}")
+    rng = np.random.default_rng(cin * 1000 + K)
+    x = rng.standard_normal((B, cin, T)).astype(np.float32)
+    W = (rng.standard_normal((cout, cin, K)) / np.sqrt(cin * K)).astype(np.float32)
+    wp = synth.pack_conv(W)
+    bias = (0.1 * rng.standard_normal(cout)).astype(np.float32) if with_bias else None
+    args = dict(stride=st, pad=pad, dil=dil, epi0=e0, epi1=e1, a0=a0, a1=a1, padded=padded)
+    knob_env.setenv("PTK_NARROW", "0")
+    generic = gpu_conv(ctx, x, wp, bias, cout, K, **args)
+    knob_env.delenv("PTK_NARROW")
+    narrow = gpu_conv(ctx, x, wp, bias, cout, K, **args)
+    assert np.all(np.isfinite(narrow))
+    assert np.array_equal(narrow, generic)
+    ref = ol.conv(x, wp, bias, cout, K, st, pad, dil, e0, e1, a0, a1)
+    assert relerr(narrow, ref) < TOL
+
+
+@pytest.mark.parametrize("case", NARROW_CONVT, ids=[f"convT{i}" for i in range(len(NARROW_CONVT))])
+def test_narrow_convT_matches_generic_and_oracle(ctx, case, knob_env):
+    """The narrow convT kernel (a delay-line step per thread, its s phases) gives the generic SIMT
+    kernel's bits on the narrow ABI shapes, and both meet the oracle bar."""
+    B, cin, tin, cout, K, st, pad, with_bias = case
+    say(f"narrow convT {case}")
+    rng = np.random.default_rng(cin * 100 + K + st)
+    x = rng.standard_normal((B, cin, tin)).astype(np.float32)
+    W = (rng.standard_normal((cin, cout, K)) * np.sqrt(st / (cin * K))).astype(np.float32)
+    wp = synth.pack_convtranspose(W, st)
+    bias = (0.1 * rng.standard_normal(cout)).astype(np.float32) if with_bias else None
+    knob_env.setenv("PTK_NARROW", "0")
+    generic = gpu_convT(ctx, x, wp, bias, cout, K, st, pad)
+    knob_env.delenv("PTK_NARROW")
+    narrow = gpu_convT(ctx, x, wp, bias, cout, K, st, pad)
+    assert np.all(np.isfinite(narrow))
+    assert np.array_equal(narrow, generic)
+    ref = ol.convT(x, wp, bias, cout, K, st, pad)
+    assert relerr(narrow, ref) < TOL
