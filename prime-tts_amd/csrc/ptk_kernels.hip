@@ -1386,9 +1386,6 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
   return 0;
 }
 
-// ------------------------------------------------------------------------------ SIMT fallbacks
-// Narrow problems (the cout = 1..15 convs of the tail, 1-channel inputs): one thread per output,
-// summing over tap then channel onto the bias in the reference's order.
 // ------------------------------------------------------------------------------ narrow convs
 // Convs and convTs with few output rows on the reference ABI path (cout4 < 16, channel counts 1,
 // 4 or 16: the PQMF synthesis FIR 4 -> 1 K 63; the iSTFT overlap-add 16 -> 1 and window sum
@@ -1590,6 +1587,9 @@ __global__ void __launch_bounds__(NARROW_THREADS) convT_narrow_kernel(
   }
 }
 
+// ------------------------------------------------------------------------------ SIMT fallbacks
+// Any shape the MFMA and narrow kernels do not take: one thread per output, summing over tap then
+// channel onto the bias in the reference's order.
 __global__ void conv_simt_kernel(const float *__restrict__ x, long long ldx, long long bsx,
                                  long long lim, int cin, const float *__restrict__ wp,
                                  const float *__restrict__ bias, int cout, int K, int st, int dil,
