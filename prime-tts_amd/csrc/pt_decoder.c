@@ -659,7 +659,8 @@ int ptd_decode_noalloc(pt_ctx *c, const ptd_model *m, const float *z, int64_t T,
            cap >> 20);
     return -1;
   }
-  if (ptk_scratch_acquire(c->g_stream)) {
+  int sdev = -1;
+  if (ptk_scratch_acquire(c->g_stream, &sdev)) {
     PT_LOG("ptd_decode_noalloc: %s", ptk_last_error());
     return -1;
   }
@@ -674,7 +675,7 @@ int ptd_decode_noalloc(pt_ctx *c, const ptd_model *m, const float *z, int64_t T,
   c->g_arena_used = u0;
   c->arena_alloc_bytes = h0;
   /* recorded even after a failure: whatever part of the decode was queued still uses the scratch */
-  if (ptk_scratch_release(c->g_stream, 1)) {
+  if (ptk_scratch_release(c->g_stream, sdev, 1)) {
     PT_LOG("ptd_decode_noalloc: %s", ptk_last_error());
     rc = -1;
   }

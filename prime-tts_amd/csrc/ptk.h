@@ -53,14 +53,14 @@ int ptk_graph_destroy(void *exec);
 #define PTK_STATIC_SCRATCH_BYTES ((size_t) 64 << 20)
 int ptk_static_scratch(void **p, size_t *bytes);
 /* Ordering of the scratch's users on one GPU: acquire makes stream s wait for the work of the
- * previous user (an event recorded after it; not while s is being captured) and holds the
- * device's lock; release records the event on s when work was queued (again not under capture)
- * and drops the lock.  Every successful acquire is followed by one release on the same thread.
- * Neither allocates. */
+ * previous user (an event recorded after it; not while s is being captured), holds the device's
+ * lock and stores the device index in *dev; release records the event on s when work was queued
+ * (again not under capture) and drops that device's lock.  Every successful acquire is followed
+ * by one release with its device index, on the same thread.  Neither allocates. */
+int ptk_scratch_acquire(void *s, int *dev);
+int ptk_scratch_release(void *s, int dev, int recorded_work);
 /* re-read the PTK_* kernel-selection knobs from the environment (otherwise read once) */
 void ptk_knobs_reload(void);
-int ptk_scratch_acquire(void *s);
-int ptk_scratch_release(void *s, int recorded_work);
 
 /* ---------------------------------------------------------------- conv problem descriptor
  * One implicit-GEMM problem.  Row m of the GEMM is an output channel (conv: m = co) or a phase

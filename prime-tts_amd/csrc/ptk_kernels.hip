@@ -114,11 +114,13 @@ static int stream_capturing(hipStream_t st, bool *on) {
   return 0;
 }
 
-extern "C" int ptk_scratch_acquire(void *s) {
+extern "C" int ptk_scratch_acquire(void *s, int *dev_out) {
   int dev = -1;
   void *p;
+  *dev_out = -1;
   if (scratch_resolve(&p) || scratch_device(&dev)) return -1;
   g_scratch_use[dev].lock();
+  *dev_out = dev;
   bool cap = false;
   hipError_t e = hipSuccess;
   if (stream_capturing((hipStream_t) s, &cap) == 0) {
@@ -127,12 +129,12 @@ extern "C" int ptk_scratch_acquire(void *s) {
     set_err("hipStreamWaitEvent on the static scratch's event failed: %s", hipGetErrorString(e));
   }
   g_scratch_use[dev].unlock();
+  *dev_out = -1;
   return -1;
 }
 
-extern "C" int ptk_scratch_release(void *s, int recorded_work) {
-  int dev = -1;
-  if (scratch_device(&dev)) return -1;
+extern "C" int ptk_scratch_release(void *s, int dev, int recorded_work) {
+  if (dev < 0 || dev >= PTK_SCRATCH_MAX_DEVICES) return -1;
   bool cap = false;
   int rc = stream_capturing((hipStream_t) s, &cap);
   if (rc == 0 && recorded_work && !cap) {
