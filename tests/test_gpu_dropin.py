@@ -136,6 +136,50 @@ def test_reference_driver_gpu_split(model, tmp_path):
     assert alloc + copy + kern + free <= total * 1.05 + 1.0
 
 
+CONV_NODES = ROOT / "tests" / "golden" / "v21_conv_nodes.json"
+
+
+def test_reference_driver_every_conv_node(model, tmp_path):
+    """The reference's C-runtime parity method (a checkpoint of every node, tests/v21_parity_c.py)
+    on the conv path: both builds of the reference driver run the case with the interpreter's node
+    fusion and device chaining off (PT_V21_FUSE=0, PT_V21_CHAIN=0: every conv and convT output
+    is materialised on the host) and dump, through the driver's checkpoint option
+    (main_v21.c:307-321), the output of each of the graph's 124 conv and 5 convT nodes
+    (tests/golden/v21_conv_nodes.json, from the reference's generated node table).  Each node of
+    the build linked against the library must be within 1e-4 x RMS of the CPU build's, with the
+    differences of every node before it carried along (encoder, flow and decoder, the device
+    matmuls included)."""
+    import json
+    d, case, _ = model
+    names = [n["name"] for n in json.loads(CONV_NODES.read_text())["nodes"]]
+    (tmp_path / "names.txt").write_text("\n".join(names) + "\n")
+    env = {"PT_V21_FUSE": "0", "PT_V21_CHAIN": "0"}
+    runs = {}
+    for label, binary, extra in (("cpu", CPU_BIN, ["--cpu"]), ("dev", DEV_BIN, [])):
+        ck = tmp_path / f"ck_{label}"
+        ck.mkdir()
+        say(f"reference driver ({label} build) with checkpoints of {len(names)} conv nodes")
+        r = _run([binary, *extra, "--container", d / "model.ptk", "--case", case, "--out",
+                  tmp_path / f"{label}.npy", "--checkpoints", tmp_path / "names.txt", "--ckdir", ck],
+                 600, env)
+        assert (tmp_path / f"{label}.npy").exists(), r.stdout[-2000:] + r.stderr[-2000:]
+        runs[label] = ck
+    worst, rows = 0.0, []
+    for nm in names:
+        f = nm.replace("/", "_") + ".npy"
+        a = np.load(runs["dev"] / f).astype(np.float64).ravel()
+        b = np.load(runs["cpu"] / f).astype(np.float64).ravel()
+        assert a.shape == b.shape, nm
+        e = float(np.max(np.abs(a - b)) / max(np.sqrt(np.mean(b ** 2)), 1e-30))
+        rows.append((e, nm))
+        worst = max(worst, e)
+    rows.sort(reverse=True)
+    for e, nm in rows[:5]:
+        say(f"  {nm}: max|err|/rms = {e:.3g}")
+    say(f"{len(names)} conv / convT nodes, worst max|err|/rms {worst:.3g}, median {rows[len(rows) // 2][0]:.3g}")
+    assert worst <= 1e-4, rows[:5]
+
+
 STREAM_FIXTURE = ROOT / "tests" / "golden" / "ref_decoder_ckpt_T198.npz"
 
 
