@@ -152,7 +152,8 @@ int ptk_conv_launch(const ptk_conv_desc *d, int ngroup, void *s);
 int ptk_conv_mfma_ok(const ptk_conv_desc *d);
 
 /* SIMT fallbacks over the PACKED layouts, for narrow shapes (cout4 < 16, tiny cin, huge K*dil):
- * conv: X rows of ldx with in-kernel padding by `shift`; convT: the phase/tap form. */
+ * conv: X rows of ldx with in-kernel padding by `shift`; convT: the phase/tap form.  The conv's
+ * epilogue codes are PTK_EPI_* without PTK_EPI_ADDT (refused: no tensor is passed). */
 int ptk_conv_simt(const float *x, int64_t ldx, int64_t bsx, int64_t lim, int cin, const float *wp,
                   const float *bias, int cout, int K, int stride, int dil, int shift, float *y,
                   int64_t ldy, int64_t bsy, int64_t n, int batch, int epi0, float a0, int epi1,

@@ -1620,6 +1620,11 @@ extern "C" int ptk_conv_simt(const float *x, int64_t ldx, int64_t bsx, int64_t l
                              int dil, int shift, float *y, int64_t ldy, int64_t bsy, int64_t n,
                              int batch, int epi0, float a0, int epi1, float a1, void *s) {
   if (n <= 0 || batch <= 0) return 0;
+  // no residual tensor reaches these kernels: a tensor add would read through a null pointer
+  if (epi0 == PTK_EPI_ADDT || epi1 == PTK_EPI_ADDT) {
+    set_err("ptk_conv_simt: epilogue code %d (tensor add) takes no tensor here", PTK_EPI_ADDT);
+    return -1;
+  }
   const long long per_wg = NARROW_THREADS;
   const long long win = (per_wg - 1) * stride + (long long) (K - 1) * dil + 1;
   const long long cs = cin >= 16 ? cin + 4 : cin;

@@ -100,3 +100,22 @@ def test_pads_in_kernel_follows_the_op_switch():
                            text=True, timeout=60)
         out[v] = int(r.stdout.strip())
     assert out == {None: 1, "conv,convT,matmul": 1, "convT": 1, "matmul": 0, "": 1}
+
+
+def test_simt_launcher_refuses_a_tensor_add_without_its_tensor():
+    """ptk_conv_simt takes epilogue codes without a residual tensor, so code 5 (tensor add) would
+    read through a null pointer on the device: refused on the host, before any HIP call."""
+    import ctypes as C
+    lib = pkg.load()
+    f = lib.ptk_conv_simt
+    f.restype = C.c_int
+    f.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_int, C.c_void_p, C.c_void_p,
+                  C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int64, C.c_int64,
+                  C.c_int64, C.c_int, C.c_int, C.c_float, C.c_int, C.c_float, C.c_void_p]
+    dummy = C.c_void_p(16)   # never dereferenced: the refusal comes first
+    for e0, e1 in ((5, 0), (1, 5)):
+        rc = f(dummy, 8, 32, 8, 4, dummy, None, 1, 3, 1, 1, 1, dummy, 8, 32, 8, 1, e0, 0.1, e1,
+               0.0, None)
+        assert rc == -1
+        lib.ptk_last_error.restype = C.c_char_p
+        assert b"tensor add" in lib.ptk_last_error()
