@@ -126,8 +126,10 @@ def _decode(ctx, model, z, stages=False):
     return out
 
 
-@pytest.mark.parametrize("T", [5, 37])
+@pytest.mark.parametrize("T", [1, 2, 5, 37])
 def test_decoder_small_vs_oracle(env, T):
+    """Every stage and the waveform against the oracle, down to one latent frame (conv_post's
+    reflect pad and the tail's trim then touch both ends of the sequence in one tile)."""
     ctx, model, ws, bs = env
     say(f"decoder T={T}")
     z = synth.latent(T, 100 + T)
