@@ -58,10 +58,12 @@ typedef struct {
   int on;
   double t;
 } phase_t;
+static int g_cudaprof;
+static pthread_once_t g_cudaprof_once = PTHREAD_ONCE_INIT;
+static void cudaprof_read(void) { g_cudaprof = getenv("PT_V21_CUDAPROF") ? 1 : 0; }
 static int cudaprof(void) {
-  static int v = -1;   /* read once; a benign race between first callers */
-  if (v < 0) v = getenv("PT_V21_CUDAPROF") ? 1 : 0;
-  return v;
+  pthread_once(&g_cudaprof_once, cudaprof_read);
+  return g_cudaprof;
 }
 static void phase_begin(phase_t *p) {
   p->on = cudaprof();
