@@ -318,6 +318,11 @@ static void tighten_timer_slack(void) {
   if (!getenv("PT_V21_SLACK0")) prctl(PR_SET_TIMERSLACK, 1UL, 0, 0, 0);
 }
 
+int ptdi_wait_before_copy(pt_ctx *c) {
+  pthread_once(&g_wait_once, wait_policy_read);
+  return g_wait_us <= 0 ? 0 : ptdi_wait(c);
+}
+
 int ptdi_wait(pt_ctx *c) {
   pthread_once(&g_wait_once, wait_policy_read);
   if (g_wait_us <= 0) return ptk_stream_sync(c->g_stream);   /* the runtime's own blocking wait */
@@ -696,7 +701,7 @@ int pt_v21_conv(pt_ctx *c, const float *X, int64_t ldx, int64_t cin, float *Y, i
     phase_end(&ph, &c->g_kernel_ms);
     return 0;
   }
-  if (ptdi_wait(c)) goto fail;
+  if (ptdi_wait_before_copy(c)) goto fail;
   if (ldy == n) {
     if (ptk_d2h_async(Y, dy, yb, c->g_stream)) goto fail;
   } else if (ptk_d2h_2d_async(Y, (size_t) ldy * sizeof(float), dy, (size_t) n * sizeof(float),
@@ -808,7 +813,7 @@ int pt_v21_convT(pt_ctx *c, const float *X, int64_t ldx, int64_t cin, int64_t ti
                             dy, Lout, (int64_t) c4 * Lout, Lout, (int) batch, c->g_stream)) {
     goto fail;
   }
-  if (ptdi_wait(c)) goto fail;
+  if (ptdi_wait_before_copy(c)) goto fail;
   if (ldy == Lout) {
     if (ptk_d2h_async(Y, dy, yb, c->g_stream)) goto fail;
   } else if (ptk_d2h_2d_async(Y, (size_t) ldy * sizeof(float), dy, (size_t) Lout * sizeof(float),
@@ -878,7 +883,7 @@ int pt_v21_matmul(pt_ctx *c, const float *A, int64_t m, int64_t k, int64_t lda, 
   int r = k > 0 && (ptk_h2d_async(dA, hA ? hA : A, (size_t) m * k * f, c->g_stream) ||
                     ptk_h2d_async(dB, hB ? hB : B, (size_t) k * nn * f, c->g_stream));
   phase_end(&ph, &c->g_copy_ms);
-  r = r || ptk_matmul(dA, m, k, k, dB, nn, nn, dC, nn, c->g_stream) || ptdi_wait(c) ||
+  r = r || ptk_matmul(dA, m, k, k, dB, nn, nn, dC, nn, c->g_stream) || ptdi_wait_before_copy(c) ||
       ptk_d2h_async(hC ? hC : C, dC, cb, c->g_stream) || ptk_stream_sync(c->g_stream);
   if (!r && hC)
     for (int64_t i = 0; i < m; i++) memcpy(C + i * ldc, hC + i * nn, (size_t) nn * f);
@@ -1016,7 +1021,7 @@ float *pt_v21_dev_upload(pt_ctx *c, const void *h, int64_t n) {
 
 void pt_v21_dev_sync_host(pt_ctx *c, void *host, const void *dev, int64_t n) {
   if (!c || n <= 0) return;
-  if (ptdi_wait(c) || ptk_d2h_async(host, dev, (size_t) n * sizeof(float), c->g_stream) ||
+  if (ptdi_wait_before_copy(c) || ptk_d2h_async(host, dev, (size_t) n * sizeof(float), c->g_stream) ||
       ptk_stream_sync(c->g_stream))
     PT_LOG("pt_v21_dev_sync_host failed: %s", ptk_last_error());
 }

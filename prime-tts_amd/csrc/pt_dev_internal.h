@@ -36,6 +36,10 @@ void ptdi_pool_ref(int delta);
 
 /* wait for the context's stream under the wait policy (PT_V21_WAIT_US); 0 / -1 */
 int ptdi_wait(pt_ctx *c);
+/* the wait ahead of a result copy that is followed by a stream synchronisation: the policy's
+ * sleep-poll when PT_V21_WAIT_US > 0, nothing under the runtime's own wait (the synchronisation
+ * after the copy waits for the kernels as well); 0 / -1 */
+int ptdi_wait_before_copy(pt_ctx *c);
 
 /* fill a conv descriptor for a plain conv over device buffers (in_op / epilogues left empty) */
 void ptdi_conv_desc(ptk_conv_desc *d, const float *x, int64_t ldx, int64_t bsx, int64_t lim,
