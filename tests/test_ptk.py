@@ -6,7 +6,6 @@ float16 values (numpy) for every non-NaN fp16 code; the reference's own C reader
 decoder's records; and refusal of each kind of corrupt file."""
 from __future__ import annotations
 
-import pathlib
 import struct
 import subprocess
 import sys
