@@ -912,11 +912,17 @@ __global__ void __launch_bounds__(64 * NW) conv_mfma_kernel(const ConvGroup g) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   };
+  // The S partial sums of a value in wave order.  Every read is issued (a wave past the split
+  // re-reads the group's first, in bounds, and is not added), so the reads of all values go out
+  // together behind one wait instead of one round trip each behind a branch.
   auto reduced = [&](int nb, int v) {
-    float sum = red_of(wg0)[(nb * NV + v) * 64 + lane];
+    const int o = (nb * NV + v) * 64 + lane;
+    float part[NW];
 #pragma unroll
-    for (int i = 1; i < NW; i++)
-      if (i < S) sum += red_of(wg0 + i)[(nb * NV + v) * 64 + lane];
+    for (int i = 0; i < NW; i++) part[i] = red_of(wg0 + (i < S ? i : 0))[o];
+    float sum = part[0];
+#pragma unroll
+    for (int i = 1; i < NW; i++) sum = i < S ? sum + part[i] : sum;
     return sum;
   };
   // Fast path: a full block whose rows are consecutive output channels (conv, or a convT block
