@@ -824,20 +824,26 @@ __global__ void __launch_bounds__(64 * NW) conv_mfma_kernel(const ConvGroup g) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      if constexpr (LD) {
-        load_chunk((chunk0 + j + 1) * CONV_CK, mask, nju);
-        PTK_PIN_VMEM();
-      }
       if constexpr (KC > 0) {
+        // the next chunk's window loads go out behind tap 0's MFMAs, not between the window
+        // store and the chunk's first MFMA
 #pragma unroll
         for (int k = 0; k < KC; k++) {
           tap(acur[k], k);
           if constexpr (LD) {
+            if (k == 0) {
+              load_chunk((chunk0 + j + 1) * CONV_CK, mask, nju);
+              PTK_PIN_VMEM();
+            }
             acur[k] = wa(k, j + 1);
             PTK_PIN_VMEM();
           }
         }
       } else {
+        if constexpr (LD) {
+          load_chunk((chunk0 + j + 1) * CONV_CK, mask, nju);
+          PTK_PIN_VMEM();
+        }
         for (int k = 0; k < K; k++) tap(wa(k, j), k);
       }
       __builtin_amdgcn_wave_barrier();
