@@ -1816,26 +1816,88 @@ static unsigned ew_blocks(long long n) {
   if (b > 8192) b = 8192;
   return (unsigned) (b < 1 ? 1 : b);
 }
+
+// The same elementwise ops four elements per thread, for 16-byte aligned operands (the decoder's
+// arena blocks are 256-byte aligned): each element goes through exactly the scalar kernel's
+// operations, the n % 4 tail elements through threads 0 .. n % 4 - 1.
+__device__ __forceinline__ float leaky1(float v, float a) { return v >= 0.0f ? v : a * v; }
+__global__ void avg3_leaky4_kernel(const float *__restrict__ a, const float *__restrict__ b,
+                                   const float *__restrict__ c, float *__restrict__ y, long long n,
+                                   float alpha) {
+  const long long n4 = n >> 2, i0 = (long long) blockIdx.x * blockDim.x + threadIdx.x;
+  const long long st = (long long) gridDim.x * blockDim.x;
+  for (long long i = i0; i < n4; i += st) {
+    const float4 va = reinterpret_cast<const float4 *>(a)[i], vb = reinterpret_cast<const float4 *>(b)[i],
+                 vc = reinterpret_cast<const float4 *>(c)[i];
+    reinterpret_cast<float4 *>(y)[i] = make_float4(leaky1(((va.x + vb.x) + vc.x) / 3.0f, alpha),
+                                                   leaky1(((va.y + vb.y) + vc.y) / 3.0f, alpha),
+                                                   leaky1(((va.z + vb.z) + vc.z) / 3.0f, alpha),
+                                                   leaky1(((va.w + vb.w) + vc.w) / 3.0f, alpha));
+  }
+  if (i0 < (n & 3)) {
+    const long long e = (n4 << 2) + i0;
+    y[e] = leaky1(((a[e] + b[e]) + c[e]) / 3.0f, alpha);
+  }
+}
+__global__ void add4_kernel(const float *__restrict__ a, const float *__restrict__ b,
+                            float *__restrict__ y, long long n, int epi, float alpha) {
+  const long long n4 = n >> 2, i0 = (long long) blockIdx.x * blockDim.x + threadIdx.x;
+  const long long st = (long long) gridDim.x * blockDim.x;
+  for (long long i = i0; i < n4; i += st) {
+    const float4 va = reinterpret_cast<const float4 *>(a)[i], vb = reinterpret_cast<const float4 *>(b)[i];
+    float4 v = make_float4(va.x + vb.x, va.y + vb.y, va.z + vb.z, va.w + vb.w);
+    if (epi == 1) v = make_float4(leaky1(v.x, alpha), leaky1(v.y, alpha), leaky1(v.z, alpha), leaky1(v.w, alpha));
+    reinterpret_cast<float4 *>(y)[i] = v;
+  }
+  if (i0 < (n & 3)) {
+    const long long e = (n4 << 2) + i0;
+    const float v = a[e] + b[e];
+    y[e] = epi == 1 ? leaky1(v, alpha) : v;
+  }
+}
+__global__ void leaky4_kernel(const float *__restrict__ a, float *__restrict__ y, long long n, float alpha) {
+  const long long n4 = n >> 2, i0 = (long long) blockIdx.x * blockDim.x + threadIdx.x;
+  const long long st = (long long) gridDim.x * blockDim.x;
+  for (long long i = i0; i < n4; i += st) {
+    const float4 va = reinterpret_cast<const float4 *>(a)[i];
+    reinterpret_cast<float4 *>(y)[i] = make_float4(leaky1(va.x, alpha), leaky1(va.y, alpha),
+                                                   leaky1(va.z, alpha), leaky1(va.w, alpha));
+  }
+  if (i0 < (n & 3)) y[(n4 << 2) + i0] = leaky1(a[(n4 << 2) + i0], alpha);
+}
+static bool al16(const void *p) { return ((uintptr_t) p & 15) == 0; }
 extern "C" int ptk_add(const float *a, const float *b, float *y, int64_t n, int epi, float alpha,
                        void *s) {
   if (n <= 0) return 0;
-  hipLaunchKernelGGL(add_kernel, dim3(ew_blocks(n)), dim3(256), 0, (hipStream_t) s, a, b, y,
-                     (long long) n, epi, alpha);
+  if (al16(a) && al16(b) && al16(y) && n >= 4)
+    hipLaunchKernelGGL(add4_kernel, dim3(ew_blocks(n >> 2)), dim3(256), 0, (hipStream_t) s, a, b, y,
+                       (long long) n, epi, alpha);
+  else
+    hipLaunchKernelGGL(add_kernel, dim3(ew_blocks(n)), dim3(256), 0, (hipStream_t) s, a, b, y,
+                       (long long) n, epi, alpha);
   HCHK(hipGetLastError());
   return 0;
 }
 extern "C" int ptk_avg3_leaky(const float *a, const float *b, const float *c, float *y, int64_t n,
                               float alpha, void *s) {
   if (n <= 0) return 0;
-  hipLaunchKernelGGL(avg3_leaky_kernel, dim3(ew_blocks(n)), dim3(256), 0, (hipStream_t) s, a, b, c,
-                     y, (long long) n, alpha);
+  if (al16(a) && al16(b) && al16(c) && al16(y) && n >= 4)
+    hipLaunchKernelGGL(avg3_leaky4_kernel, dim3(ew_blocks(n >> 2)), dim3(256), 0, (hipStream_t) s, a,
+                       b, c, y, (long long) n, alpha);
+  else
+    hipLaunchKernelGGL(avg3_leaky_kernel, dim3(ew_blocks(n)), dim3(256), 0, (hipStream_t) s, a, b,
+                       c, y, (long long) n, alpha);
   HCHK(hipGetLastError());
   return 0;
 }
 extern "C" int ptk_leaky(const float *a, float *y, int64_t n, float alpha, void *s) {
   if (n <= 0) return 0;
-  hipLaunchKernelGGL(leaky_kernel, dim3(ew_blocks(n)), dim3(256), 0, (hipStream_t) s, a, y,
-                     (long long) n, alpha);
+  if (al16(a) && al16(y) && n >= 4)
+    hipLaunchKernelGGL(leaky4_kernel, dim3(ew_blocks(n >> 2)), dim3(256), 0, (hipStream_t) s, a, y,
+                       (long long) n, alpha);
+  else
+    hipLaunchKernelGGL(leaky_kernel, dim3(ew_blocks(n)), dim3(256), 0, (hipStream_t) s, a, y,
+                       (long long) n, alpha);
   HCHK(hipGetLastError());
   return 0;
 }

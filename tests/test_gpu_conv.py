@@ -499,3 +499,48 @@ def test_narrow_convT_matches_generic_and_oracle(ctx, case, knob_env):
     assert np.array_equal(narrow, generic)
     ref = ol.convT(x, wp, bias, cout, K, st, pad)
     assert relerr(narrow, ref) < TOL
+
+
+@pytest.mark.parametrize("n", [4, 7, 1027, 462848 + 3])
+def test_elementwise_vector_and_scalar_kernels_agree(ctx, n):
+    """The elementwise glue (branch average + LeakyReLU, add (+ LeakyReLU), LeakyReLU) runs four
+    elements per thread on 16-byte aligned operands and one per thread otherwise: both give the
+    bits of numpy's float32 arithmetic in the same order (((a + b) + c) / 3, then the slope), the
+    n % 4 tail included."""
+    say(f"elementwise n={n}")
+    lib = ctx.lib
+    VP, I64 = C.c_void_p, C.c_int64
+    for name, args in (("ptk_avg3_leaky", [VP, VP, VP, VP, I64, C.c_float, VP]),
+                       ("ptk_add", [VP, VP, VP, I64, C.c_int, C.c_float, VP]),
+                       ("ptk_leaky", [VP, VP, I64, C.c_float, VP])):
+        getattr(lib, name).argtypes = args
+        getattr(lib, name).restype = C.c_int
+    rng = np.random.default_rng(n)
+    a, b, c = (rng.standard_normal(n).astype(np.float32) for _ in range(3))
+    s = ctx.get_ptr("g_stream")
+    f32 = np.float32
+    alpha = f32(0.1)
+
+    def leaky(v):
+        return np.where(v >= 0, v, alpha * v).astype(np.float32)
+
+    want = {"avg3": leaky(((a + b) + c) / f32(3.0)), "add": leaky(a + b), "add0": (a + b),
+            "leaky": leaky(a)}
+    for off in (0, 1):   # 0: 16-byte aligned (four per thread), 1: one float in (one per thread)
+        bufs = [pkg.DevBuf(n + 1) for _ in range(4)]
+        for buf, h in zip(bufs[:3], (a, b, c)):
+            buf.upload(ctx, np.concatenate([np.zeros(off, np.float32), h]))
+        pa, pb, pc, py = (buf.ptr + 4 * off for buf in bufs)
+        got = {}
+        assert lib.ptk_avg3_leaky(pa, pb, pc, py, n, alpha, s) == 0
+        got["avg3"] = bufs[3].download(ctx)[off:off + n]
+        assert lib.ptk_add(pa, pb, py, n, 1, alpha, s) == 0
+        got["add"] = bufs[3].download(ctx)[off:off + n]
+        assert lib.ptk_add(pa, pb, py, n, 0, alpha, s) == 0
+        got["add0"] = bufs[3].download(ctx)[off:off + n]
+        assert lib.ptk_leaky(pa, py, n, alpha, s) == 0
+        got["leaky"] = bufs[3].download(ctx)[off:off + n]
+        for k, v in want.items():
+            assert np.array_equal(got[k].view(np.uint32), v.view(np.uint32)), (k, off)
+        for buf in bufs:
+            buf.free()
