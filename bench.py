@@ -195,7 +195,7 @@ def decode_conv_gflop(T):
     return sum(f * c for f, c in zip(_COL_FLOP, cols)) / 1e9
 
 
-_DECODER_KERNELS = ("conv_mfma_kernel", "avg3_leaky_kernel", "tail_kernel")
+_DECODER_KERNELS = ("conv_mfma_kernel", "avg3_leaky_kernel", "avg3_leaky4_kernel", "tail_kernel")
 GRBM_XCDS, SIMDS = 8, 1024     # GRBM_GUI_ACTIVE sums the 8 XCDs; 256 CUs x 4 SIMDs
 
 

@@ -20,7 +20,8 @@ def _bench():
 
 def _kernel_of(name):
     if name.startswith("branch avg"):
-        return "avg3_leaky_kernel(float const*, float const*, float const*, float*, long long, float)"
+        # the decoder's operands are aligned: the four-wide form of the branch average
+        return "avg3_leaky4_kernel(float const*, float const*, float const*, float*, long long, float)"
     if name.startswith("tail"):
         return "tail_kernel(float const*, long long, long long, long long, float*, long long)"
     return "void conv_mfma_kernel<11, 1, 0>(ConvGroup)"
