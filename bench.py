@@ -592,15 +592,15 @@ def main():
             tp.free(); tw.free()
             log(f"kernel loop: {args.kernel_loop} tail launches (L {TAIL_L}, batch {tb}) done")
         narrow_abi_loop(pkg, lib, ctx, args.kernel_loop)
-        # calibration for the HBM byte counters: add_kernel over 64 Mi floats reads exactly
-        # 512 MiB and writes 256 MiB per launch
+        # calibration for the HBM byte counters: the elementwise add over 64 Mi floats (aligned
+        # buffers: add4_kernel, four per thread) reads exactly 512 MiB and writes 256 MiB per launch
         n = 64 << 20
         a, b2, y = pkg.DevBuf(n), pkg.DevBuf(n), pkg.DevBuf(n)
         for _ in range(5):
             if lib.pt_v21_devadd_run(ctx.ptr, a.ptr, b2.ptr, y.ptr, n, 0, 0.0) != 0:
                 raise RuntimeError("calibration add failed")
         ctx.sync()
-        log("calibration: 5 add_kernel launches of 64 Mi floats (read 524288 KiB, write 262144 KiB)")
+        log("calibration: 5 add4_kernel launches of 64 Mi floats (read 524288 KiB, write 262144 KiB)")
         return
     for _ in range(5):
         run_depth()
