@@ -999,10 +999,13 @@ __global__ void __launch_bounds__(64 * NW) conv_mfma_kernel(const ConvGroup g) {
         if (gg < ngrp)
 #pragma unroll
           for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++) val[i] += reduced(nb, v0 + i);
-#pragma unroll 1
-      for (int e = 0; e < ep.nepi; e++) {
+      // the chain op by op over the four slots (straight-line: a rolled loop over the ops made the
+      // compiler copy the value array at every op); a slot past nepi is skipped by a uniform branch
+#pragma unroll
+      for (int e = 0; e < PTK_MAX_EPI; e++) {
+        if (e >= ep.nepi) break;
         const int op = (ep.ops >> (4 * e)) & 15;
-        const float a = e == 0 ? ep.a[0] : e == 1 ? ep.a[1] : e == 2 ? ep.a[2] : ep.a[3];
+        const float a = ep.a[e];
         if (op == PTK_EPI_LEAKY) {
 #pragma unroll
           for (int gg = 0; gg < NG; gg++)
@@ -1033,22 +1036,12 @@ __global__ void __launch_bounds__(64 * NW) conv_mfma_kernel(const ConvGroup g) {
             if (gg < ngrp)
 #pragma unroll
               for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++) val[i] = val[i] / a;
-        } else if (op == PTK_EPI_ADDT) {
-          if (e == addt) {
+        } else if (op == PTK_EPI_ADDT) {   // the chain's one tensor add (the launcher's rule)
 #pragma unroll
-            for (int gg = 0; gg < NG; gg++)
-              if (gg < ngrp)
+          for (int gg = 0; gg < NG; gg++)
+            if (gg < ngrp)
 #pragma unroll
-                for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++) val[i] = val[i] + rv[i];
-          } else {   // a second tensor add (no decoder layer has one): its operand read directly
-            const ptk_epi &ee = d.epi[e];
-#pragma unroll
-            for (int gg = 0; gg < NG; gg++)
-              if (gg < ngrp)
-#pragma unroll
-                for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++)
-                val[i] = val[i] + ee.t[(long long) b * ee.bst + (row0 + lrow + urow(i)) * ee.ldt + clof(cbo(i))];
-          }
+              for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++) val[i] = val[i] + rv[i];
         }
       }
       // a group shares its column block, so one test covers its stores
@@ -1350,14 +1343,18 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
     const bool one_phase = d->C4 == d->M || d->C4 % rb == 0;
     pi.div_phase = fast_div(d->C4 == d->M ? 1u : (unsigned) (d->C4 / rb > 0 ? d->C4 / rb : 1));
     pi.addt = -1;
+    int naddt = 0;
     for (int e = 0; e < d->nepi; e++)
-      if (pi.addt < 0 && d->epi[e].op == PTK_EPI_ADDT) pi.addt = e;
+      if (d->epi[e].op == PTK_EPI_ADDT && naddt++ == 0) pi.addt = e;
     pi.M = d->M;
     // the fast epilogue's 32-bit indices: columns, and byte offsets from a row block's first row
     const long long lim31 = 1LL << 31, lim30 = 1LL << 30;
     bool fast = one_phase && d->ldy < (1LL << 23) && d->Lout < lim30 &&
                 (d->q0 + d->nq + d->ext_r) * d->ys + d->C4 < lim30 && d->q0 - d->ext_l >= 0 &&
                 ((long long) rb * d->ldy + d->Lout) * 4 < lim31;
+    // the fast epilogue reads one tensor operand (loaded ahead of the reduction); a chain with two
+    // takes the general path
+    if (naddt > 1) fast = false;
     if (pi.addt >= 0) {
       const long long ldt = d->epi[pi.addt].ldt;
       fast = fast && ldt >= 0 && ldt < (1LL << 23) && ((long long) rb * ldt + d->Lout) * 4 < lim31;
