@@ -15,7 +15,7 @@ timed on this host on a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
        python bench.py --kernel-loop N   (only the dominant kernel and the tail kernel, N launches
-                                          each: for rocprofv3 --pmc)
+                                          each after a clock warm-up: for rocprofv3)
        python bench.py --decode-loop N [--batch B]   (N config-4 decodes, for a kernel trace)
        python bench.py --layer-table KERNEL_TRACE_CSV [--batch B] [--counters COUNTER_CSV]
                                           (per-launch table of that trace, MFMA utilisation from a
@@ -77,9 +77,35 @@ class EventTimer:
     def __init__(self, pkg, ctx):
         self.lib, self.ctx = pkg.load(), ctx
         self.e0, self.e1 = self.lib.ptd_event_create(), self.lib.ptd_event_create()
+        self.w = [self.lib.ptd_event_create(), self.lib.ptd_event_create()]
 
-    def time(self, fn, reps, warmup=0):
-        """ms per call of fn over reps calls, after warmup untimed calls on the same stream."""
+    def warm(self, fn, ms=None):
+        """Untimed calls of fn issued for `ms` of host time (WARM_MS), the device kept busy: after
+        an idle spell the MI355X's clock climbs for ~30 ms of sustained load, and launches timed
+        inside that climb run up to 15 % slower.  The stream is not drained afterwards: the timed
+        calls queue behind these (small launches issued into a just-drained stream ran ~20 %
+        slower for their first hundred or so)."""
+        ms = WARM_MS if ms is None else ms
+        t0 = time.perf_counter()
+        k = 0
+        while (time.perf_counter() - t0) * 1e3 < ms:
+            t1 = time.perf_counter()
+            for _ in range(16):
+                fn()
+                if (time.perf_counter() - t1) * 1e3 >= 1.0:
+                    break
+            # at most two batches (16 calls or 1 ms of issue each) queued: wait for the end of the
+            # previous batch (elapsed time of an event to itself waits for it), then mark the end
+            # of this one
+            if k:
+                self.lib.ptd_event_elapsed_ms(self.w[(k - 1) & 1], self.w[(k - 1) & 1])
+            self.lib.ptd_event_record(self.ctx.ptr, self.w[k & 1])
+            k += 1
+
+    def time(self, fn, reps, warmup=0, warm_ms=None):
+        """ms per call of fn over reps calls, after WARM_MS (or warm_ms) of untimed calls and then
+        warmup more untimed calls on the same stream."""
+        self.warm(fn, warm_ms)
         for _ in range(warmup):
             fn()
         self.lib.ptd_event_record(self.ctx.ptr, self.e0)
@@ -92,8 +118,8 @@ class EventTimer:
         return ms / reps
 
     def close(self):
-        self.lib.ptd_event_destroy(self.e0)
-        self.lib.ptd_event_destroy(self.e1)
+        for e in [self.e0, self.e1] + self.w:
+            self.lib.ptd_event_destroy(e)
 
 
 def mrf_depth_setup(pkg, ctx, stage, T):
@@ -125,7 +151,16 @@ def tail_bytes(L, batch):
     return 4.0 * batch * (72 * L + 16 * (L - 1))
 
 
-DECODE_LOOP_WARM = 3
+# Untimed load before each timed leg: the chip's clock reaches its sustained value ~30 ms into a
+# run of launches after an idle spell (the dominant launch: 28-30 us per launch for the first
+# ~7 ms, 24.3 us from ~30 ms on).
+WARM_MS = 60.0
+
+
+def decode_loop_warm(batch):
+    """Warm-up decodes of `--decode-loop` (dropped from its layer table): about WARM_MS of load at
+    ~0.3 ms per request."""
+    return max(3, int(WARM_MS / (0.3 * batch)))
 
 # The 19 launches of one decode at T = 226 frames, in issue order (pt_decoder.c decode_impl), with
 # the algorithmic work of one request: flop for the conv launches (the MRF entries are grouped
@@ -199,7 +234,7 @@ _DECODER_KERNELS = ("conv_mfma_kernel", "avg3_leaky_kernel", "avg3_leaky4_kernel
 GRBM_XCDS, SIMDS = 8, 1024     # GRBM_GUI_ACTIVE sums the 8 XCDs; 256 CUs x 4 SIMDs
 
 
-def _decodes(rows):
+def _decodes(rows, batch):
     """Decoder dispatches (weight relayouts and copies excluded) in issue order, cut into decodes
     of 19, the warm-up decodes dropped."""
     rows = sorted(rows, key=lambda r: int(r["Dispatch_Id"]))
@@ -207,10 +242,10 @@ def _decodes(rows):
     n = len(DECODE_LAUNCHES)
     if len(ks) % n:
         raise SystemExit(f"{len(ks)} decoder dispatches is not a multiple of {n}")
-    return [ks[i:i + n] for i in range(0, len(ks), n)][DECODE_LOOP_WARM:]
+    return [ks[i:i + n] for i in range(0, len(ks), n)][decode_loop_warm(batch):]
 
 
-def _mfma_util(counter_csv):
+def _mfma_util(counter_csv, batch):
     """Per launch position: mean MFMA utilisation, SQ_VALU_MFMA_BUSY_CYCLES /
     (GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs) (rocprofv3's MfmaUtil), from a --pmc pass over the
     same decode loop."""
@@ -219,7 +254,7 @@ def _mfma_util(counter_csv):
     for r in csv.DictReader(open(counter_csv)):
         e = by.setdefault(r["Dispatch_Id"], {"Dispatch_Id": r["Dispatch_Id"], "Kernel_Name": r["Kernel_Name"]})
         e[r["Counter_Name"]] = float(r["Counter_Value"])
-    dec = _decodes(list(by.values()))
+    dec = _decodes(list(by.values()), batch)
     out = []
     for i in range(len(DECODE_LAUNCHES)):
         u = [d[i]["SQ_VALU_MFMA_BUSY_CYCLES"] / (d[i]["GRBM_GUI_ACTIVE"] / GRBM_XCDS * SIMDS) for d in dec]
@@ -233,10 +268,10 @@ def layer_table(csv_path, batch, counter_csv=None):
     SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE over the same loop, the MFMA utilisation too."""
     import csv
     rows = [r for r in csv.DictReader(open(csv_path)) if r.get("Kind", "KERNEL_DISPATCH") == "KERNEL_DISPATCH"]
-    dec = _decodes(rows)
-    util = _mfma_util(counter_csv) if counter_csv else None
+    dec = _decodes(rows, batch)
+    util = _mfma_util(counter_csv, batch) if counter_csv else None
     head = "| # | launch | kernel | us | rate | % of peak |" + (" MFMA util % |" if util else "")
-    out = [f"{len(dec)} decodes of T = 226 x batch {batch} (after {DECODE_LOOP_WARM} warm-up decodes)", "",
+    out = [f"{len(dec)} decodes of T = 226 x batch {batch} (after {decode_loop_warm(batch)} warm-up decodes)", "",
            head, "|---" * (7 if util else 6) + "|"]
     tot_us = tot_flop = 0.0
     for i, (name, kind, work) in enumerate(DECODE_LAUNCHES):
@@ -563,11 +598,11 @@ def main():
         B = args.batch
         dz = pkg.DevBuf.of(ctx, np.stack([pkg.synth.latent(226, 226 + i) for i in range(B)]))
         dw = pkg.DevBuf(B * HOP * 226)
-        for _ in range(DECODE_LOOP_WARM + args.decode_loop):
+        for _ in range(decode_loop_warm(B) + args.decode_loop):
             if lib.ptd_decode(ctx.ptr, model.ptr, dz.ptr, 226, B, dw.ptr) != 0:
                 raise RuntimeError("decode failed")
         ctx.sync()
-        log(f"decode loop: {DECODE_LOOP_WARM} + {args.decode_loop} decodes of T 226 x {B} done")
+        log(f"decode loop: {decode_loop_warm(B)} + {args.decode_loop} decodes of T 226 x {B} done")
         return
 
     # ---------------------------------------------------------------- dominant kernel
@@ -576,21 +611,29 @@ def main():
     bufs, xin, xinl, a_s, ys = mrf_depth_setup(pkg, ctx, 0, 904)
     run_depth = lambda: lib.ptd_mrf_depth(ctx.ptr, model.ptr, 0, 2, xin, xinl, a_s, ys, None, 904)  # noqa: E731
     if args.kernel_loop:
-        for _ in range(args.kernel_loop):
+        N = args.kernel_loop
+        # the narrow late stages too: the fused tail kernel at config 4's shape, N launches of one
+        # request and N of 64 requests at once (256- and 1024-sample tiles); buffers made first, so
+        # the loops below run back to back
+        tails = [(tb,) + tuple(tail_setup(pkg, ctx, TAIL_L, tb)) for tb in (1, 64)]
+        tail_call = lambda tb, tp, tw: lib.ptd_tail(ctx.ptr, model.ptr, tp.ptr, TAIL_L, tb, tw.ptr)  # noqa: E731
+        # the clock first: WARM_MS of the batch-64 tail, a kernel of its own, so that every conv
+        # dispatch of a trace of this loop is a measured one (an elementwise add of the same
+        # length did not bring the clock up for the MFMA launches: 27.5 us per conv launch after
+        # it, 24.8 after the tail, 24.3 after the conv itself)
+        timer.warm(lambda: tail_call(*tails[1]))
+        for _ in range(N):
             if run_depth() != 0:
                 raise RuntimeError("mrf depth failed")
-        ctx.sync()
-        log(f"kernel loop: {2 * args.kernel_loop} launches done")
-        # the narrow late stages: the fused tail kernel at config 4's shape, as many launches of
-        # one request and of 64 requests at once (256- and 1024-sample tiles)
-        for tb in (1, 64):
-            tp, tw = tail_setup(pkg, ctx, TAIL_L, tb)
-            for _ in range(args.kernel_loop):
-                if lib.ptd_tail(ctx.ptr, model.ptr, tp.ptr, TAIL_L, tb, tw.ptr) != 0:
+        for tb, tp, tw in tails:
+            for _ in range(N):
+                if tail_call(tb, tp, tw) != 0:
                     raise RuntimeError("tail failed")
-            ctx.sync()
+        ctx.sync()
+        for _, tp, tw in tails:
             tp.free(); tw.free()
-            log(f"kernel loop: {args.kernel_loop} tail launches (L {TAIL_L}, batch {tb}) done")
+        log(f"kernel loop: {WARM_MS:.0f} ms of the batch-64 tail, then {2 * N} conv launches, "
+            f"{N} tail launches of batch 1 and {N} of batch 64 done")
         narrow_abi_loop(pkg, lib, ctx, args.kernel_loop)
         # calibration for the HBM byte counters: the elementwise add over 64 Mi floats (aligned
         # buffers: add4_kernel, four per thread) reads exactly 512 MiB and writes 256 MiB per launch
@@ -602,8 +645,6 @@ def main():
         ctx.sync()
         log("calibration: 5 add4_kernel launches of 64 Mi floats (read 524288 KiB, write 262144 KiB)")
         return
-    for _ in range(5):
-        run_depth()
     ms_depth = timer.time(run_depth, 50)
     ms_launch = ms_depth / 2.0
     achieved = flop_launch / (ms_launch * 1e-3) / 1e12

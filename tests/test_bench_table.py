@@ -52,11 +52,15 @@ def _write_trace(path, bench, ndec, us_of, extra_first=True):
             w.writerow(["KERNEL_DISPATCH", "Agent 1", 1, 1, 7, k + 1, 3, name, k + 1, t0, t1])
 
 
-def test_layer_table_averages_after_warmup(tmp_path):
+@pytest.mark.parametrize("batch", [1, 8])
+def test_layer_table_averages_after_warmup(tmp_path, batch):
+    """The warm-up decodes (about 60 ms of load: more of them at batch 1) are cut before the
+    per-position averages."""
     bench = _bench()
     n = len(bench.DECODE_LAUNCHES)
     assert n == 19
-    warm = bench.DECODE_LOOP_WARM
+    warm = bench.decode_loop_warm(batch)
+    assert warm >= 3 and (batch == 1 or warm < bench.decode_loop_warm(1))
 
     # warm-up decodes are 10x slower; measured decodes alternate 10 us / 30 us at position i
     def us_of(dec, i):
@@ -65,7 +69,7 @@ def test_layer_table_averages_after_warmup(tmp_path):
 
     p = tmp_path / "trace.csv"
     _write_trace(p, bench, warm + 4, us_of)
-    text = bench.layer_table(str(p), 1)
+    text = bench.layer_table(str(p), batch)
     lines = [ln for ln in text.splitlines() if ln.startswith("| ") and ln[2].isdigit()]
     assert len(lines) == n
     for i, ln in enumerate(lines):
@@ -73,9 +77,9 @@ def test_layer_table_averages_after_warmup(tmp_path):
         assert int(cells[0]) == i
         # decodes warm..warm+3 are even/odd alternately: mean of (10+i, 30+i) = 20+i
         assert float(cells[3]) == pytest.approx(20.0 + i, abs=0.01)
-    # conv_pre: 311 MFLOP in 20 us
+    # conv_pre: 311 MFLOP per request in 20 us
     first = [c.strip() for c in lines[0].strip("|").split("|")]
-    assert first[4] == f"{2 * 512 * 192 * 7 * 226 / 20e-6 / 1e12:.1f} TFLOP/s"
+    assert first[4] == f"{batch * 2 * 512 * 192 * 7 * 226 / 20e-6 / 1e12:.1f} TFLOP/s"
     assert "sum of kernel times" in text
 
 
@@ -97,7 +101,7 @@ def test_layer_table_mfma_util_from_counters(tmp_path):
     """--counters: per launch position, SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 x 1024)
     averaged over the measured decodes; '-' for the launches without MFMA work."""
     bench = _bench()
-    warm = bench.DECODE_LOOP_WARM
+    warm = bench.decode_loop_warm(1)
     trace = tmp_path / "trace.csv"
     _write_trace(trace, bench, warm + 2, lambda dec, i: 10.0)
     cols = ["Correlation_Id", "Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"]
