@@ -141,3 +141,74 @@ def test_bench_refuses_more_than_one_gpu():
     assert r.returncode == 2
     assert "one GPU" in r.stderr
     assert r.stdout == ""
+
+
+class _FakeLib:
+    """The four event calls EventTimer makes, logged in order; a call of the timed function is
+    logged by the test's own fn."""
+
+    def __init__(self):
+        self.log, self.n = [], 0
+
+    def ptd_event_create(self):
+        self.n += 1
+        return f"e{self.n}"
+
+    def ptd_event_record(self, stream, e):
+        self.log.append(("record", e))
+        return 0
+
+    def ptd_event_elapsed_ms(self, e0, e1):
+        self.log.append(("wait", e1))
+        return 1.0
+
+    def ptd_event_destroy(self, e):
+        pass
+
+
+class _FakeCtx:
+    ptr = "ctx"
+
+    def __init__(self, log):
+        self.log = log
+
+    def sync(self):
+        self.log.append(("sync", None))
+
+
+def test_warm_keeps_the_stream_fed(monkeypatch):
+    """EventTimer.warm issues the function for about WARM_MS of host time in batches of at most 16
+    calls, waits only for the previous batch's end event (never drains the stream), and a timed
+    call after it follows without a synchronisation."""
+    bench = _bench()
+    lib = _FakeLib()
+    pkg = type("P", (), {"load": staticmethod(lambda: lib)})
+    t = bench.EventTimer(pkg, _FakeCtx(lib.log))
+    clock = [0.0]
+    monkeypatch.setattr(bench.time, "perf_counter", lambda: clock[0])
+
+    def fn():
+        lib.log.append(("call", None))
+        clock[0] += 0.0002      # 0.2 ms of host time per call: a batch ends at 16 calls
+
+    t.warm(fn, ms=20.0)
+    calls = [k for k, _ in lib.log if k == "call"]
+    assert len(calls) >= 100                      # ~20 ms at 0.2 ms per call
+    assert ("sync", None) not in lib.log
+    # between two event records there are at most 16 calls, and every wait names the event
+    # recorded one batch earlier
+    recorded, since = [], 0
+    for kind, e in lib.log:
+        if kind == "call":
+            since += 1
+            assert since <= 16
+        elif kind == "record":
+            recorded.append(e)
+            since = 0
+        elif kind == "wait":
+            assert recorded and e == recorded[-1]
+    assert set(recorded) == set(t.w)
+    lib.log.clear()
+    ms = t.time(fn, 5, warm_ms=0.0)
+    assert ms == pytest.approx(1.0 / 5)
+    assert ("sync", None) not in lib.log
