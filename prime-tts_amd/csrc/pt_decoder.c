@@ -948,11 +948,12 @@ static int win_parts(int n) {
   return p < 1 ? 1 : p;
 }
 
-/* the batched run of full-width windows, on one stream or split over several */
-static int win_batch(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, const win_plan *pl,
-                     int win, int ctx, float *wav) {
-  int parts = win_parts(pl->nfull);
-  /* every part's region must fit in the arena at once; else the run stays on one stream */
+/* Parts of the batched run of full-width windows this context can run at once: win_parts, as
+ * long as every part's region fits in the arena (else 1), and the extra streams for them (*xo,
+ * NULL for one part). */
+static int win_split(pt_ctx *c, const win_plan *pl, int win, aux_t **xo) {
+  *xo = NULL;
+  int parts = pl->nfull ? win_parts(pl->nfull) : 1;
   if (parts > 1) {
     size_t need = 0;
     for (int p = 0; p < parts; p++)
@@ -961,12 +962,22 @@ static int win_batch(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, c
         ? c->g_arena_bytes - al256(c->g_arena_used) : 0;
     if (need > free_b) parts = 1;
   }
-  aux_t *x = parts > 1 ? aux_get(c, parts - 1) : NULL;
-  if (!x) return win_range(c, m, z, T, pl, pl->b0, pl->nfull, win, ctx, wav);
-  /* the extra streams start after everything queued on the context's stream so far */
+  if (parts > 1 && !(*xo = aux_get(c, parts - 1))) parts = 1;
+  return parts;
+}
+
+/* the extra streams start after everything queued on the context's stream so far */
+static int win_fork(pt_ctx *c, aux_t *x, int parts) {
   if (ptk_event_record(x->fork, c->g_stream)) return -1;
   for (int k = 0; k < parts - 1; k++)
     if (ptk_stream_wait_event(x->s[k], x->fork)) return -1;
+  return 0;
+}
+
+/* the batched run of full-width windows in `parts` parts (the extra streams already forked) */
+static int win_batch(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, const win_plan *pl,
+                     int win, int ctx, float *wav, int parts, aux_t *x) {
+  if (parts < 2) return win_range(c, m, z, T, pl, pl->b0, pl->nfull, win, ctx, wav);
   void *s0 = c->g_stream;
   const size_t used0 = c->g_arena_used;
   size_t used = used0;
@@ -1028,11 +1039,24 @@ int ptdi_decode_windows(pt_ctx *c, const ptd_model *m, const float *z, int64_t T
       *t_first = ptdi_now_ms();
     }
   }
+  aux_t *x = NULL;
+  const int parts = rc == 0 ? win_split(c, &pl, win, &x) : 1;
+  /* The extra streams fork ahead of the shorter last window when its activations lie inside the
+   * first part's region (it runs on the context's stream, before that part): the other parts then
+   * start at once instead of behind it, and a stream that shares its hardware queue with other
+   * requests does not hold their packets while it waits. */
+  int forked = 0;
+  if (rc == 0 && parts > 1 && pl.has_last &&
+      ptd_decode_arena_bytes(pl.wl.w, 1) <= al256(ptd_decode_arena_bytes(win, pl.nfull / parts + (pl.nfull % parts ? 1 : 0)))) {
+    rc = win_fork(c, x, parts);
+    forked = 1;
+  }
   /* the shorter last window before the batched run: a small decode that leaves most of the chip
    * to other streams is better early than as the tail of the request (windows write disjoint
    * samples) */
   if (rc == 0 && pl.has_last) rc = win_one(c, m, z, T, &pl.wl, wav);
-  if (rc == 0 && pl.nfull) rc = win_batch(c, m, z, T, &pl, win, ctx, wav);
+  if (rc == 0 && parts > 1 && !forked) rc = win_fork(c, x, parts);
+  if (rc == 0 && pl.nfull) rc = win_batch(c, m, z, T, &pl, win, ctx, wav, parts, x);
   if (rc) PT_LOG("windowed decode failed: %s", ptk_last_error());
   return rc;
 }

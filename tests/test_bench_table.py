@@ -212,3 +212,9 @@ def test_warm_keeps_the_stream_fed(monkeypatch):
     ms = t.time(fn, 5, warm_ms=0.0)
     assert ms == pytest.approx(1.0 / 5)
     assert ("sync", None) not in lib.log
+    # a blocker goes in after the warm-up calls and before the start event
+    lib.log.clear()
+    t.time(fn, 3, warmup=2, warm_ms=0.0, blocker=lambda: lib.log.append(("blocker", None)))
+    kinds = [k if k != "record" else e for k, e in lib.log]
+    assert kinds[:5] == ["call", "call", "blocker", t.e0, "call"]
+    assert kinds[-2:] == [t.e1, "wait"]
