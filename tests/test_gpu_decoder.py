@@ -504,7 +504,9 @@ def test_window_streams_change_no_sample(env, T, mode, knob_env):
     for runs of 16 windows or more; PTD_WINDOW_STREAMS=2 splits any run of two, =1 none) gives the
     same samples as the unsplit run, bit for bit, with the context's arena poisoned first; and a
     decode queued on the context right after it, which reuses the arena the second half used,
-    still matches its own reference (it waits for the second stream)."""
+    still matches its own reference (it waits for the second stream).  Every T here ends in a
+    clipped window, decoded on the context's stream inside the first half's arena region while
+    the second half already runs (the split forks ahead of it)."""
     ctx, model, ws, bs = env
     say(f"window streams T={T} mode={mode}")
     lib = ctx.lib
