@@ -168,8 +168,11 @@ ptd_model *ptdi_model_build(pt_ctx *c, const void *const *w, const int *wisz, co
         ? ptk_h2d_async(tmp, w[i], (size_t) wn[i] * 4, c->g_stream)
         : (ptk_h2d_async(tmp16, w[i], (size_t) wn[i] * 2, c->g_stream) ||
            ptk_h2f((float *) tmp, (const uint16_t *) tmp16, wn[i], c->g_stream));
-    if (up || ptk_relayout((float *) (base + off_w[i]), tmp, M, K, g.cin, c->g_stream) ||
-        ptk_relayout16((float *) (base + off_w16[i]), tmp, M, K, g.cin, c->g_stream) ||
+    /* the convTs' rows interleaved by phase (ptk_conv_desc.phase_il): each lane then writes its
+     * column's four phases as consecutive samples */
+    const int il = g.convT ? M / 4 : 0;
+    if (up || ptk_relayout_il((float *) (base + off_w[i]), tmp, M, K, g.cin, il, c->g_stream) ||
+        ptk_relayout16_il((float *) (base + off_w16[i]), tmp, M, K, g.cin, il, c->g_stream) ||
         ptk_h2d_async(base + off_b[i], b[i], (size_t) g.cout * sizeof(float), c->g_stream) ||
         ptk_stream_sync(c->g_stream))
       goto fail;
@@ -571,6 +574,7 @@ static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t ld
   /* ups.0 */
   ptdi_convT_desc(&d, h, T, 512 * T, T, 512, m->wr[1], m->b[1], 256, 4, 6, 16, x0, T1, 256 * T1, batch);
   d.w16 = m->wr16[1];
+  d.phase_il = 1;
   d.y2 = x0L;
   d.a2 = 0.1f;
   if (cp) cols_apply(&d, &cp->up0);
@@ -589,6 +593,7 @@ static int decode_impl(pt_ctx *c, const ptd_model *m, const float *z, int64_t ld
   ptdi_convT_desc(&d, av0, T1, 256 * T1, T1, 256, m->wr[20], m->b[20], 128, 4, 6, 16, x1, T2,
                   128 * T2, batch);
   d.w16 = m->wr16[20];
+  d.phase_il = 1;
   d.y2 = x1L;
   d.a2 = 0.1f;
   if (cp) cols_apply(&d, &cp->up1);
@@ -698,6 +703,7 @@ static int layer_run(pt_ctx *c, const ptd_model *m, int layer, const float *x, i
     ptdi_convT_desc(&d, x, T, (int64_t) g.cin * T, T, g.cin, m->wr[layer], m->b[layer], g.cout,
                     g.sd, g.pad, g.K, y, Lout, (int64_t) c4 * Lout, batch);
     d.w16 = m->wr16[layer];
+    d.phase_il = 1;
   } else {
     conv_layer_desc(&d, m, layer, x, T, T, batch, y, T);
   }

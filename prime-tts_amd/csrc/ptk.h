@@ -110,6 +110,10 @@ typedef struct {
   int K, dil, stride, shift;
   int M;                      /* GEMM rows (cout4 or s*cout4) */
   int C4;                     /* rows per phase (conv: M) */
+  /* stride-4 convT only, 0 otherwise: the rows are interleaved by phase (row m is phase m & 3 of
+     channel m >> 2; weights relaid by ptk_relayout_il / ptk_relayout16_il with il = C4), so the
+     four phases of an output column sit in one lane and go to four consecutive samples */
+  int phase_il;
   int64_t q0, nq;             /* output columns [q0, q0 + nq) */
   /* Per-item column ranges (overlap-save windows compute only the columns their kept samples
      depend on): batch item 0 starts ext_l columns earlier, the last item ends ext_r columns
@@ -141,6 +145,10 @@ int ptk_relayout(float *dst, const float *wp, int M, int K, int cin, void *s);
 /* the copy for 16-row tiles: [Mp/16][K][cinp/8][64][2], Mp = M rounded up to 16 */
 size_t ptk_relayout16_floats(int M, int K, int cin);
 int ptk_relayout16(float *dst, const float *wp, int M, int K, int cin, void *s);
+/* the same two layouts with a stride-4 convT's rows interleaved by phase (il = its rows per
+   phase C4, M = 4 * il): relaid row m is packed row (m & 3) * il + (m >> 2) */
+int ptk_relayout_il(float *dst, const float *wp, int M, int K, int cin, int il, void *s);
+int ptk_relayout16_il(float *dst, const float *wp, int M, int K, int cin, int il, void *s);
 /* fp16 -> fp32 expansion of n items (bit-exact: subnormals keep their value, inf / NaN keep sign
  * and payload, nothing is quieted) */
 int ptk_h2f(float *dst, const uint16_t *src, int64_t n, void *s);

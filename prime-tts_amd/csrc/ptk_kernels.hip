@@ -356,8 +356,12 @@ extern "C" size_t ptk_relayout_floats(int M, int K, int cin) {
   return Mp * (size_t) K * (size_t) ptk_conv_cinp(cin);
 }
 
+// il: 0, or the rows per phase C4 of a stride-4 convT whose rows the MFMA layout interleaves by
+// phase: relaid row m is packed row (m & 3) * il + (m >> 2), phase m & 3 of channel m >> 2.
+__device__ __forceinline__ int relayout_row(int m, int il) { return il ? (m & 3) * il + (m >> 2) : m; }
+
 __global__ void relayout_kernel(float *__restrict__ dst, const float *__restrict__ wp, int M,
-                                int K, int cin, int cinp, long long total) {
+                                int K, int cin, int cinp, long long total, int il) {
   long long i = (long long) blockIdx.x * blockDim.x + threadIdx.x;
   const long long st = (long long) gridDim.x * blockDim.x;
   const int nchunk = cinp / CONV_CK;
@@ -372,19 +376,34 @@ __global__ void relayout_kernel(float *__restrict__ dst, const float *__restrict
     const int m = mb * 32 + (lane & 31);
     const int ci = chunk * CONV_CK + 2 * p + (lane >> 5);
     float v = 0.0f;
-    if (m < M && ci < cin) v = wp[(((long long) (m >> 2) * K + k) * cin + ci) * 4 + (m & 3)];
+    if (m < M && ci < cin) {
+      const int ms = relayout_row(m, il);
+      v = wp[(((long long) (ms >> 2) * K + k) * cin + ci) * 4 + (ms & 3)];
+    }
     dst[i] = v;
   }
 }
 
-extern "C" int ptk_relayout(float *dst, const float *wp, int M, int K, int cin, void *s) {
+static int relayout_il_ok(int M, int il, const char *who) {
+  if (il != 0 && (il < 1 || M != 4 * il)) {
+    set_err("%s: phase interleave needs M = 4 x rows per phase (M %d, rows per phase %d)", who, M, il);
+    return 0;
+  }
+  return 1;
+}
+
+extern "C" int ptk_relayout_il(float *dst, const float *wp, int M, int K, int cin, int il, void *s) {
+  if (!relayout_il_ok(M, il, "ptk_relayout_il")) return -1;
   const long long total = (long long) ptk_relayout_floats(M, K, cin);
   long long blocks = (total + 255) / 256;
   if (blocks > 4096) blocks = 4096;
   hipLaunchKernelGGL(relayout_kernel, dim3((unsigned) blocks), dim3(256), 0, (hipStream_t) s, dst,
-                     wp, M, K, cin, ptk_conv_cinp(cin), total);
+                     wp, M, K, cin, ptk_conv_cinp(cin), total, il);
   HCHK(hipGetLastError());
   return 0;
+}
+extern "C" int ptk_relayout(float *dst, const float *wp, int M, int K, int cin, void *s) {
+  return ptk_relayout_il(dst, wp, M, K, cin, 0, s);
 }
 
 // The same weights for 16-row tiles on v_mfma_f32_16x16x4_f32: [Mp/16][K][cinp/8][64][2] (Mp = M
@@ -398,7 +417,7 @@ extern "C" size_t ptk_relayout16_floats(int M, int K, int cin) {
 }
 
 __global__ void relayout16_kernel(float *__restrict__ dst, const float *__restrict__ wp, int M,
-                                  int K, int cin, int cinp, long long total) {
+                                  int K, int cin, int cinp, long long total, int il) {
   long long i = (long long) blockIdx.x * blockDim.x + threadIdx.x;
   const long long st = (long long) gridDim.x * blockDim.x;
   const int nchunk = cinp / CONV_CK;
@@ -413,19 +432,26 @@ __global__ void relayout16_kernel(float *__restrict__ dst, const float *__restri
     const int m = mb * 16 + (lane & 15);
     const int ci = chunk * CONV_CK + 4 * s + (lane >> 4);
     float v = 0.0f;
-    if (m < M && ci < cin) v = wp[(((long long) (m >> 2) * K + k) * cin + ci) * 4 + (m & 3)];
+    if (m < M && ci < cin) {
+      const int ms = relayout_row(m, il);
+      v = wp[(((long long) (ms >> 2) * K + k) * cin + ci) * 4 + (ms & 3)];
+    }
     dst[i] = v;
   }
 }
 
-extern "C" int ptk_relayout16(float *dst, const float *wp, int M, int K, int cin, void *s) {
+extern "C" int ptk_relayout16_il(float *dst, const float *wp, int M, int K, int cin, int il, void *s) {
+  if (!relayout_il_ok(M, il, "ptk_relayout16_il")) return -1;
   const long long total = (long long) ptk_relayout16_floats(M, K, cin);
   long long blocks = (total + 255) / 256;
   if (blocks > 4096) blocks = 4096;
   hipLaunchKernelGGL(relayout16_kernel, dim3((unsigned) blocks), dim3(256), 0, (hipStream_t) s,
-                     dst, wp, M, K, cin, ptk_conv_cinp(cin), total);
+                     dst, wp, M, K, cin, ptk_conv_cinp(cin), total, il);
   HCHK(hipGetLastError());
   return 0;
+}
+extern "C" int ptk_relayout16(float *dst, const float *wp, int M, int K, int cin, void *s) {
+  return ptk_relayout16_il(dst, wp, M, K, cin, 0, s);
 }
 
 // ------------------------------------------------------------------------------ fp16 expansion
@@ -511,7 +537,7 @@ struct ConvProb {
   FastDiv div_tiles;              // by mt * nt (tiles of a middle batch item)
   FastDiv div_mt;                 // by mt
   FastDiv div_phase;              // by C4 / RB (row blocks per convT phase) when one_phase
-  int flags;                      // PROB_ONE_PHASE | PROB_FAST
+  int flags;                      // PROB_ONE_PHASE | PROB_FAST | PROB_PHASE_IL
   int ext_l;                      // item 0's first column is q0 - ext_l
   int addt;                       // the chain's first tensor add, or -1
   int M;                          // GEMM rows
@@ -520,6 +546,8 @@ struct ConvProb {
 #define PROB_ONE_PHASE 1
 // output / residual index ranges fit the 32-bit epilogue
 #define PROB_FAST 2
+// stride-4 convT with its rows interleaved by phase (row m: phase m & 3 of channel m >> 2)
+#define PROB_PHASE_IL 4
 static_assert(sizeof(ConvProb) == 64, "one 64-byte scalar load");
 
 // What the fast epilogue reads, 128 bytes per problem, fetched in one batch of scalar loads when
@@ -649,6 +677,9 @@ __global__ void __launch_bounds__(64 * NW) conv_mfma_kernel(const ConvGroup g) {
   // lies inside one phase.
   const bool phase_rows = d.C4 != d.M;
   const bool one_phase = (pi.flags & PROB_ONE_PHASE) != 0;
+  // rows interleaved by phase: only the 4-tap convT phase form (KT = 4) carries that code, so the
+  // other instantiations compile exactly as without it (the launcher refuses it elsewhere)
+  const bool phase_il = KT == 4 && (pi.flags & PROB_PHASE_IL) != 0;
   const int r_tile = phase_rows && one_phase ? fdiv(mb, pi.div_phase) : 0;
   // Lane l < RB loads the bias of the block's row l once the first chunk's loads are in flight,
   // and the epilogue fetches each value's bias from the lane of its row (ds_bpermute): the load's
@@ -661,7 +692,8 @@ __global__ void __launch_bounds__(64 * NW) conv_mfma_kernel(const ConvGroup g) {
     const int nbias = d.nbias, Mr = d.M, C4r = d.C4;
     const int m = mb * RB + lane;
     int co = m - r_tile * C4r;   // conv: r_tile = 0
-    if (!one_phase) co = m % C4r;
+    if (phase_il) co = m >> 2;
+    else if (!one_phase) co = m % C4r;
     if (lane < RB && bp != nullptr && m < Mr && co < nbias) bias_r = bp[co];
   };
   // bias of row `row` of the block (every lane of the wave must be active)
@@ -938,15 +970,17 @@ __global__ void __launch_bounds__(64 * NW) conv_mfma_kernel(const ConvGroup g) {
   // loads are issued before the reduction barrier, at a clamped column so that every lane loads
   // in bounds without a branch (a lane whose column does not exist stores nothing).  The values
   // of a lane are val[i], i < nv: value v0 + i of the block.  The chain runs op by op over all of
-  // them, one branch per op.
-  if ((pi.flags & PROB_FAST) && one_phase && mb * RB + RB <= pi.M) {
+  // them, one branch per op.  A convT block with its rows interleaved by phase (phase_il) holds
+  // RB / 4 whole channels; its stores are laid out below.
+  if ((pi.flags & PROB_FAST) && (one_phase || phase_il) && mb * RB + RB <= pi.M) {
     const ConvEpi ep = g.ep[p];
     // a wave finishes at most NMAX values (NV over the smallest split of its workgroup size),
     // in groups of GRP that share a column block (nv is a multiple of GRP)
     constexpr int NMAX = NW == 8 ? NV / 8 : NV;
     constexpr int GRP = (RB == 32 ? 4 : 2) < NMAX ? (RB == 32 ? 4 : 2) : NMAX, NG = NMAX / GRP;
     const int ngrp = nv / GRP;
-    const long long row0 = (long long) mb * RB - (long long) r_tile * ep.C4;   // first channel
+    // first channel of the block
+    const long long row0 = phase_il ? (long long) mb * (RB / 4) : (long long) mb * RB - (long long) r_tile * ep.C4;
     const int ldy32 = ep.ldy, ldt32 = ep.ldt;
     float *yk = const_cast<float *>(ep.y) + (long long) b * ep.bsy + row0 * ldy32;
     const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
@@ -964,13 +998,15 @@ __global__ void __launch_bounds__(64 * NW) conv_mfma_kernel(const ConvGroup g) {
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) {
       // columns of this lane: one per column block (RB = 32), two (RB = 16)
-      bool ok[NCB];
-      int cl[NCB];
+      bool ok[NCB], oq[NCB];
+      int cl[NCB], cu[NCB];
 #pragma unroll
       for (int cb = 0; cb < NCB; cb++) {
         const int q = (int) q0 + 32 * nb + (RB == 32 ? l32 : 16 * cb + l16);
         const int col = q * ep.ys + r_tile - ep.ypad;
-        ok[cb] = q < qend32 && col >= 0 && col < ep.lout;
+        oq[cb] = q < qend32;
+        cu[cb] = col;   // phase_il: the sample of phase 0 (r_tile = 0), unclamped
+        ok[cb] = oq[cb] && col >= 0 && col < ep.lout;
         cl[cb] = ok[cb] ? col : 0;
       }
       auto cbo = [&](int i) { return RB == 32 ? 0 : ((v0 + i) >> 2); };
@@ -1044,6 +1080,57 @@ __global__ void __launch_bounds__(64 * NW) conv_mfma_kernel(const ConvGroup g) {
               for (int jj = 0, i = gg * GRP; jj < GRP; jj++, i++) val[i] = val[i] + rv[i];
         }
       }
+      if (phase_il) {
+        // Rows interleaved by phase: the GRP values of a group are consecutive phases p0 .. of one
+        // channel at one column (RB = 32: channel 2 * (v >> 2) + half of the block; RB = 16:
+        // channel quad, column block v >> 2), so they go to GRP consecutive samples.  Stored in
+        // pairs, 8 bytes from one lane, where both samples exist; one by one at the sequence
+        // ends.  Every address is formed from an existing sample (0 otherwise).
+        const int chl = RB == 32 ? half : quad;
+        auto cuof = [&](int c) { return NCB == 1 || c == 0 ? cu[0] : cu[NCB - 1]; };
+        auto oqof = [&](int c) { return NCB == 1 || c == 0 ? oq[0] : oq[NCB - 1]; };
+        typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+        for (int gg = 0; gg < NG; gg++)
+          if (gg < ngrp) {
+            const int vg = v0 + gg * GRP, cb = cbo(gg * GRP);
+            const unsigned so = (unsigned) ((RB == 32 ? 2 * (vg >> 2) : 0) * ldy32) * 4u;
+            const bool inq = oqof(cb);
+            if constexpr (GRP == 1) {   // one value per wave (16-row tiles, 8-way split)
+              const int sa = cuof(cb) + (vg & 3);
+              if (inq && sa >= 0 && sa < ep.lout) {
+                const unsigned vo = (unsigned) (chl * ldy32 + sa) * 4u;
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val[gg]), ry, vo, so, 0);
+                if (ep.y2 != nullptr)
+                  __builtin_amdgcn_raw_buffer_store_b32(
+                      __float_as_uint(val[gg] >= 0.0f ? val[gg] : ep.a2 * val[gg]), ry2, vo, so, 0);
+              }
+              continue;
+            }
+#pragma unroll
+            for (int jj = 0; jj < GRP; jj += 2) {
+              const int i = gg * GRP + jj;
+              const int sa = cuof(cb) + (vg & 3) + jj;   // sample of value i; value i + 1 at sa + 1
+              const bool va = inq && sa >= 0 && sa < ep.lout;
+              const bool vb = inq && sa + 1 >= 0 && sa + 1 < ep.lout;
+              const int sb = va ? sa : (vb ? sa + 1 : 0);
+              const unsigned vo = (unsigned) (chl * ldy32 + sb) * 4u;
+              const float y2a = val[i] >= 0.0f ? val[i] : ep.a2 * val[i];
+              const float y2b = val[i + 1] >= 0.0f ? val[i + 1] : ep.a2 * val[i + 1];
+              if (va && vb) {
+                __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(val[i]), __float_as_uint(val[i + 1])}, ry, vo, so, 0);
+                if (ep.y2 != nullptr)
+                  __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(y2a), __float_as_uint(y2b)}, ry2, vo, so, 0);
+              } else if (va || vb) {
+                const float one = va ? val[i] : val[i + 1];
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(one), ry, vo, so, 0);
+                if (ep.y2 != nullptr)
+                  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(va ? y2a : y2b), ry2, vo, so, 0);
+              }
+            }
+          }
+        continue;
+      }
       // a group shares its column block, so one test covers its stores
 #pragma unroll
       for (int gg = 0; gg < NG; gg++)
@@ -1069,7 +1156,10 @@ __global__ void __launch_bounds__(64 * NW) conv_mfma_kernel(const ConvGroup g) {
     const long long q = q0 + vcol(nb, v);
     if (m >= M || q >= qend) return;
     int co = m, r = 0;
-    if (phase_rows) {
+    if (phase_il) {
+      r = m & 3;
+      co = m >> 2;
+    } else if (phase_rows) {
       r = m / C4;
       co = m - r * C4;
     }
@@ -1296,6 +1386,12 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
               "resource", d->K, d->cin);
       return -1;
     }
+    if (d->phase_il && !(d->M == 4 * d->C4 && d->ys == 4 && d->dil == -1 && d->stride == 1 &&
+                         d->K == 4 && ngroup == 1)) {
+      set_err("ptk_conv_launch: rows interleaved by phase need a single stride-4 convT in the "
+              "4-tap phase form (M %d, rows per phase %d, %d taps)", d->M, d->C4, d->K);
+      return -1;
+    }
     if (d->in_op != PTK_IN_PLAIN && !(d->in_a >= 0.0f && d->in_a <= 1.0f)) {
       set_err("ptk_conv_launch: input LeakyReLU slope %g outside [0, 1]", (double) d->in_a);
       return -1;
@@ -1340,7 +1436,8 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
     if (pi.count > maxcount) maxcount = pi.count;
     pi.div_tiles = fast_div((unsigned) (pi.mt * pi.nt));
     pi.div_mt = fast_div((unsigned) pi.mt);
-    const bool one_phase = d->C4 == d->M || d->C4 % rb == 0;
+    const bool il = d->phase_il != 0;
+    const bool one_phase = !il && (d->C4 == d->M || d->C4 % rb == 0);
     pi.div_phase = fast_div(d->C4 == d->M ? 1u : (unsigned) (d->C4 / rb > 0 ? d->C4 / rb : 1));
     pi.addt = -1;
     int naddt = 0;
@@ -1349,17 +1446,20 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
     pi.M = d->M;
     // the fast epilogue's 32-bit indices: columns, and byte offsets from a row block's first row
     const long long lim31 = 1LL << 31, lim30 = 1LL << 30;
-    bool fast = one_phase && d->ldy < (1LL << 23) && d->Lout < lim30 &&
+    bool fast = (one_phase || il) && d->ldy < (1LL << 23) && d->Lout < lim30 &&
                 (d->q0 + d->nq + d->ext_r) * d->ys + d->C4 < lim30 && d->q0 - d->ext_l >= 0 &&
                 ((long long) rb * d->ldy + d->Lout) * 4 < lim31;
     // the fast epilogue reads one tensor operand (loaded ahead of the reduction); a chain with two
     // takes the general path
     if (naddt > 1) fast = false;
+    // the interleaved-phase stores have no tensor-add operand loads: such a chain takes the
+    // general path
+    if (il && pi.addt >= 0) fast = false;
     if (pi.addt >= 0) {
       const long long ldt = d->epi[pi.addt].ldt;
       fast = fast && ldt >= 0 && ldt < (1LL << 23) && ((long long) rb * ldt + d->Lout) * 4 < lim31;
     }
-    pi.flags = (one_phase ? PROB_ONE_PHASE : 0) | (fast ? PROB_FAST : 0);
+    pi.flags = (one_phase ? PROB_ONE_PHASE : 0) | (fast ? PROB_FAST : 0) | (il ? PROB_PHASE_IL : 0);
     pi.ext_l = (int) d->ext_l;
     ConvEpi &ep = g.ep[i];
     ep.y = d->y;
