@@ -1192,14 +1192,15 @@ static int win_max(int nb) { return nb == 2 ? WinGeo<2>::XWMAX : WinGeo<1>::XWMA
 // (tests that change a knob between calls); each is an atomic int, so a launch running meanwhile
 // sees the old or the new value of each knob.
 enum KnobId {
-  KN_CONV_SPLIT, KN_CONV_RB, KN_CONV_S8, KN_CONV_S8_MAX, KN_CONV_NB, KN_TAIL_OUT, KN_TAIL_GRID,
-  KN_TAIL_XCD, KN_NARROW, KN_COUNT
+  KN_CONV_SPLIT, KN_CONV_RB, KN_CONV_S8, KN_CONV_S8_MAX, KN_CONV_NB, KN_CONV_FAST, KN_TAIL_OUT,
+  KN_TAIL_GRID, KN_TAIL_XCD, KN_NARROW, KN_COUNT
 };
 static const struct {
   const char *name;
   int dflt;
 } kKnobs[KN_COUNT] = {{"PTK_CONV_SPLIT", 0}, {"PTK_CONV_RB", 0},    {"PTK_CONV_S8", 1},
-                      {"PTK_CONV_S8_MAX", 1536}, {"PTK_CONV_NB", 0}, {"PTK_TAIL_OUT", 0},
+                      {"PTK_CONV_S8_MAX", 1536}, {"PTK_CONV_NB", 0}, {"PTK_CONV_FAST", 1},
+                      {"PTK_TAIL_OUT", 0},
                       {"PTK_TAIL_GRID", 0},   {"PTK_TAIL_XCD", 1},  {"PTK_NARROW", 1}};
 static std::atomic<int> g_knob[KN_COUNT];
 static std::once_flag g_knob_once;
@@ -1453,8 +1454,13 @@ extern "C" int ptk_conv_launch(const ptk_conv_desc *dd, int ngroup, void *stream
     // takes the general path
     if (naddt > 1) fast = false;
     // the interleaved-phase stores have no tensor-add operand loads: such a chain takes the
-    // general path
-    if (il && pi.addt >= 0) fast = false;
+    // general path, and so do outputs where a sample pair is not 8-byte aligned (64-bit stores)
+    if (il && (pi.addt >= 0 || ((d->ldy | d->bsy) & 1) != 0 || ((uintptr_t) d->y & 7) != 0 ||
+               ((uintptr_t) d->y2 & 7) != 0))
+      fast = false;
+    // PTK_CONV_FAST=0: every block through the general per-element epilogue (tests compare the
+    // two epilogues)
+    if (!knob(KN_CONV_FAST)) fast = false;
     if (pi.addt >= 0) {
       const long long ldt = d->epi[pi.addt].ldt;
       fast = fast && ldt >= 0 && ldt < (1LL << 23) && ((long long) rb * ldt + d->Lout) * 4 < lim31;

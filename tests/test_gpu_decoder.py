@@ -367,6 +367,53 @@ def test_tile_shapes_vs_oracle(env, rb, split, knob_env):
     assert np_ref.sndr(wav, ref) >= 60.0
 
 
+@pytest.mark.parametrize("rb,split", [(0, 0), (16, 4), (16, 8), (32, 8)])
+def test_general_epilogue_matches_fast(env, rb, split, knob_env):
+    """The per-element epilogue (every block forced onto it with PTK_CONV_FAST=0) writes the fast
+    epilogue's bits: a conv with a LeakyReLU epilogue, both convTs (the decoder's rows
+    interleaved by phase, whose fast path stores sample pairs), conv_post with its partial row
+    block, an MRF stack (residual adds) and whole decodes at batch 2 (the convTs' LeakyReLU
+    copies, the branch averages); on the launcher's tiles and forced 16-row / 8-way ones."""
+    ctx, model, ws, bs = env
+    say(f"general vs fast epilogue rb={rb} split={split}")
+    if rb:
+        knob_env.setenv("PTK_CONV_RB", str(rb))
+        knob_env.setenv("PTK_CONV_SPLIT", str(split))
+    lib = ctx.lib
+
+    def run_all():
+        outs = []
+        for layer, T, in_a, epi_a in [(0, 226, 0.0, 0.1), (1, 61, 0.1, 0.0), (20, 97, 0.1, 0.0),
+                                      (39, 203, 0.0, 0.0)]:
+            g = synth.dec_layer(layer)
+            x = np.random.default_rng(layer).standard_normal((g["cin"], T)).astype(np.float32)
+            c4 = (g["cout"] + 3) // 4 * 4
+            tout = 4 * T if g.get("convT") else T
+            dx, dy = dev_of(ctx, x), pkg.DevBuf(c4 * tout)
+            assert lib.ptd_layer(ctx.ptr, model.ptr, layer, dx.ptr, T, 1, dy.ptr, in_a, epi_a) == 0
+            outs.append(dy.download(ctx))
+            dx.free(); dy.free()
+        x = np.random.default_rng(3).standard_normal((128, 300)).astype(np.float32)
+        dx, dy = dev_of(ctx, x), pkg.DevBuf(128 * 300)
+        assert lib.ptd_mrf(ctx.ptr, model.ptr, 1, dx.ptr, 300, 0.1, dy.ptr) == 0
+        outs.append(dy.download(ctx))
+        dx.free(); dy.free()
+        for T in (3, 45):
+            z = np.stack([synth.latent(T, 600 + T), synth.latent(T, 700 + T)])
+            dz, dw = dev_of(ctx, z), pkg.DevBuf(2 * 256 * T)
+            assert lib.ptd_decode(ctx.ptr, model.ptr, dz.ptr, T, 2, dw.ptr) == 0
+            outs.append(dw.download(ctx))
+            dz.free(); dw.free()
+        return outs
+
+    fast = run_all()
+    knob_env.setenv("PTK_CONV_FAST", "0")
+    general = run_all()
+    knob_env.delenv("PTK_CONV_FAST")
+    for i, (a, b) in enumerate(zip(fast, general)):
+        assert np.array_equal(a, b), i
+
+
 def _oracle_windows(ws, bs, z, win, ctx_):
     """The reference's overlap-save schedule (main_v21_serve.c:229-257) composed on the oracle."""
     T = z.shape[-1]
