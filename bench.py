@@ -397,7 +397,7 @@ def sndr_db(est, ref):
     return float("inf") if err == 0.0 else float(10.0 * np.log10(float(np.sum(ref ** 2)) / err))
 
 
-def cpu_baseline(pkg, gpu_wavs=None, gpu_long=None):
+def cpu_baseline(pkg, gpu_wavs=None, gpu_long=None, gpu_226=None):
     """The reference's own CPU conv path (oracle/_ref, built from the reference sources) inside the
     oracle's decoder driver, or the C restatement when _ref is absent.  Timed two ways: config 5's
     eight requests as eight host threads pinned to eight distinct cores (the reference's
@@ -405,7 +405,8 @@ def cpu_baseline(pkg, gpu_wavs=None, gpu_long=None):
     gpu_wavs: the same eight requests' waveforms from the timed GPU step, compared (SNDR) with the
     CPU ones.  gpu_long: the timed step's stitched long-form windows (T = 1500, 96/16), compared
     with one full decode of the same latents on the same CPU path, its conv nodes split over the
-    host's threads (bit-identical to one thread; untimed)."""
+    host's threads (bit-identical to one thread; untimed).  gpu_226: a GPU waveform of
+    the config-4 latents, compared with the single-thread decode."""
     sys.path.insert(0, str(ROOT / "tests"))
     import oracle_lib as ol
     ws, bs = pkg.synth.decoder_weights(1234)
@@ -422,7 +423,7 @@ def cpu_baseline(pkg, gpu_wavs=None, gpu_long=None):
     T = 226
     z = pkg.synth.latent(T, 226)
     t0 = time.perf_counter()
-    ol.decoder(ws, bs, z, use_ref=use_ref)
+    wav226 = ol.decoder(ws, bs, z, use_ref=use_ref)
     dt1 = time.perf_counter() - t0
     audio1 = T * HOP / SR
     layers = _cpu_layers(pkg, ol, ws, bs, use_ref, cores[0])
@@ -446,7 +447,8 @@ def cpu_baseline(pkg, gpu_wavs=None, gpu_long=None):
             # the same requests' waveforms from the timed GPU step against these CPU ones
             "sndr_vs_gpu_db": [round(sndr_db(g, c), 2) for g, c in zip(gpu_wavs, cpu_wavs)]
             if gpu_wavs is not None else None,
-            "longform_sndr_vs_gpu_db": long_db}
+            "longform_sndr_vs_gpu_db": long_db,
+            "config4_sndr_vs_gpu_db": round(sndr_db(gpu_226, wav226), 2) if gpu_226 is not None else None}
 
 
 MATMUL_SHAPES = [(37, 53, 29), (120, 192, 120), (120, 96, 192)]   # m, k, n: encoder attention
@@ -510,6 +512,50 @@ def _cpu_model():
     except OSError:
         pass
     return "unknown"
+
+
+def streams8_leg(pkg, lib, ctx, model, args):
+    """Config 4's request shape on 8 concurrent streams: 8 contexts of a ptd_server, each driven by
+    its own pthread, one T = 226 decode each (the latents of the batch-8 leg), after 60 ms of the
+    same.  Returns the figures, whether every stream's waveform equals the batched decode's item
+    bit for bit, and stream 0's waveform (the config-4 latents)."""
+    T, n = 226, 8
+    zs = [pkg.synth.latent(T, 226 + i) for i in range(n)]
+    dz = [pkg.DevBuf.of(ctx, z) for z in zs]
+    dw = [pkg.DevBuf(HOP * T) for _ in range(n)]
+    reqs = (pkg.Request * n)(*[pkg.Request(dz[i].ptr, dw[i].ptr, T, 0, 0) for i in range(n)])
+    srv = lib.ptd_server_create(n, int(lib.ptd_decode_arena_bytes(T, 1)) + (16 << 20))
+    if not srv:
+        raise RuntimeError("ptd_server_create failed")
+    wall = C.c_double()
+
+    def step():
+        if lib.ptd_serve_run(srv, model.ptr, reqs, n, C.byref(wall)) != 0:
+            raise RuntimeError("serve run failed")
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < WARM_MS:
+        step()
+    lib.ptd_device_sync()
+    steps = max(args.steps, 20)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    lib.ptd_device_sync()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    lib.ptd_server_destroy(srv)
+    wavs = [b.download(ctx) for b in dw]
+    db = pkg.DevBuf.of(ctx, np.concatenate(zs))
+    wb = pkg.DevBuf(n * HOP * T)
+    if lib.ptd_decode(ctx.ptr, model.ptr, db.ptr, T, n, wb.ptr) != 0:
+        raise RuntimeError("batched decode failed")
+    batched = wb.download(ctx).reshape(n, -1)
+    same = all(np.array_equal(wavs[i], batched[i]) for i in range(n))
+    for b in dz + dw + [db, wb]:
+        b.free()
+    return ({"config4_8streams_ms_per_step": round(ms, 4),
+             "config4_8streams_audio_s_per_s": round(n * T * HOP / SR / (ms * 1e-3), 2),
+             "config4_8streams_decoder_tflops": round(n * 32.571e9 / (ms * 1e-3) / 1e12, 3),
+             "equal_batched_decode": same}, wavs[0])
 
 
 def queue_leg(pkg, lib, model, zs, wv, Ts, T_long, arena, args):
@@ -874,6 +920,12 @@ def main():
     log(f"queue: {queue}")
     for b in zs + wv:
         b.free()
+    # the north star's own case: the T = 226 request on 8 concurrent streams (made after config
+    # 5's, so that leg's streams land on the hardware queues they always did)
+    streams8, c4_wav0 = streams8_leg(pkg, lib, ctx, model, args)
+    parity["config4_8streams_equal_batched_decode"] = streams8.pop("equal_batched_decode")
+    log(f"config 4 on 8 streams: {streams8}")
+    cfg.update(streams8)
 
     out = {
         "metric": "decoder audio-sec/sec at 8 streams (+ conv TFLOP/s, % fp32-MFMA peak)",
@@ -924,7 +976,8 @@ def main():
     out["parity"] = parity
     if not args.no_cpu_baseline:
         log("cpu baseline (reference conv path: 8 pinned threads, then 1 thread for config 4 and configs 1-3) ...")
-        out["cpu_baseline"] = cpu_baseline(pkg, c5_wavs[:8], c5_wavs[-1])
+        out["cpu_baseline"] = cpu_baseline(pkg, c5_wavs[:8], c5_wavs[-1], c4_wav0)
+        parity["config4_8streams_vs_reference_cpu_sndr_db"] = out["cpu_baseline"].pop("config4_sndr_vs_gpu_db")
         snd = out["cpu_baseline"].pop("sndr_vs_gpu_db")
         parity["config5_requests_vs_reference_cpu_sndr_db"] = {"min": min(snd), "per_request": snd}
         parity["config5_longform_windows_vs_reference_cpu_full_decode_sndr_db"] = \
