@@ -640,9 +640,13 @@ __global__ void __launch_bounds__(64 * NW) conv_mfma_kernel(const ConvGroup g) {
   // as long as the largest problem's workgroup count, and the excess of a shorter one exits.
   const int p = blockIdx.y;
   const ConvProb pi = g.info[p];
+  const ptk_conv_desc &d = g.d[p];
+  // The scalar-cache lines of the problem's descriptor fields the prologue reads (x .. q0) and of
+  // the split are touched in the same batch of loads as the launch facts: the prologue's later
+  // reads of them then hit, instead of each batch waiting out a round trip of its own.
+  asm volatile("" ::"s"(pi.count), "s"(d.x), "s"(d.w16), "s"(d.q0), "s"(g.split));
   const int bid = blockIdx.x;
   if (bid >= pi.count) return;
-  const ptk_conv_desc &d = g.d[p];
   const int mt = pi.mt;
   // Tiles item after item, column tile after column tile, row block fastest: item 0 has nt0
   // column tiles, the middle items nt, the last one ntl >= nt (all nt for a plain launch).
