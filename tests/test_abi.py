@@ -119,3 +119,20 @@ def test_simt_launcher_refuses_a_tensor_add_without_its_tensor():
         assert rc == -1
         lib.ptk_last_error.restype = C.c_char_p
         assert b"tensor add" in lib.ptk_last_error()
+
+
+def test_phase_interleaved_relayout_refuses_a_wrong_phase_count():
+    """ptk_relayout_il interleaves the rows of a stride-4 convT (row m: phase m & 3 of channel
+    m >> 2), which needs M = 4 x the rows per phase: any other count is refused on the host,
+    before any HIP call, for both the 32-row and the 16-row layouts."""
+    import ctypes as C
+    lib = pkg.load()
+    lib.ptk_last_error.restype = C.c_char_p
+    dummy = C.c_void_p(16)   # never dereferenced: the refusal comes first
+    for name in ("ptk_relayout_il", "ptk_relayout16_il"):
+        f = getattr(lib, name)
+        f.restype = C.c_int
+        f.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p]
+        for M, il in ((512, 100), (512, 256), (510, 128), (512, -1)):
+            assert f(dummy, dummy, M, 4, 256, il, None) == -1, (name, M, il)
+            assert b"phase interleave" in lib.ptk_last_error()
