@@ -17,6 +17,8 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
        python bench.py --kernel-loop N   (only the dominant kernel and the tail kernel, N launches
                                           each after a clock warm-up: for rocprofv3)
        python bench.py --decode-loop N [--batch B]   (N config-4 decodes, for a kernel trace)
+       python bench.py --streams8-loop N   (N steps of the T = 226 request on 8 concurrent
+                                          streams after ~60 ms of the same, for a kernel trace)
        python bench.py --layer-table KERNEL_TRACE_CSV [--batch B] [--counters COUNTER_CSV]
                                           (per-launch table of that trace, MFMA utilisation from a
                                           --pmc pass over the same loop)
@@ -514,7 +516,7 @@ def _cpu_model():
     return "unknown"
 
 
-def streams8_leg(pkg, lib, ctx, model, args):
+def streams8_leg(pkg, lib, ctx, model, args, steps=None):
     """Config 4's request shape on 8 concurrent streams: 8 contexts of a ptd_server, each driven by
     its own pthread, one T = 226 decode each (the latents of the batch-8 leg), after 60 ms of the
     same.  Returns the figures, whether every stream's waveform equals the batched decode's item
@@ -536,7 +538,7 @@ def streams8_leg(pkg, lib, ctx, model, args):
     while (time.perf_counter() - t0) * 1e3 < WARM_MS:
         step()
     lib.ptd_device_sync()
-    steps = max(args.steps, 20)
+    steps = steps or max(args.steps, 20)
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
@@ -625,6 +627,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-loop", type=int, default=0)
     ap.add_argument("--decode-loop", type=int, default=0)
+    ap.add_argument("--streams8-loop", type=int, default=0)
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--layer-table", metavar="KERNEL_TRACE_CSV")
     ap.add_argument("--counters", metavar="COUNTER_COLLECTION_CSV")
@@ -654,6 +657,11 @@ def main():
                 raise RuntimeError("decode failed")
         ctx.sync()
         log(f"decode loop: {decode_loop_warm(B)} + {args.decode_loop} decodes of T 226 x {B} done")
+        return
+
+    if args.streams8_loop:
+        fig, _ = streams8_leg(pkg, lib, ctx, model, args, steps=args.streams8_loop)
+        log(f"8-stream loop: {args.streams8_loop} steps after the warm-up: {fig}")
         return
 
     # ---------------------------------------------------------------- dominant kernel
