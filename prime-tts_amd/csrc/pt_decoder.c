@@ -374,9 +374,10 @@ static int cone_plan_make(cone_plan *cp, int64_t T, int batch, const ptk_emit *e
   return 0;
 }
 
-/* Windowed-decode knobs (PTD_WINDOW_CONE, PTD_WINDOW_STREAMS, PTD_WINDOW_PARTS): read once per
+/* Windowed-decode knobs (PTD_WINDOW_CONE, PTD_WINDOW_STREAMS, PTD_WINDOW_PARTS) and the servers'
+ * stream placement (PTD_SERVER_PLACE=0: off): read once per
  * process, re-read by ptdi_decoder_knobs_reload (tests that change one between calls). */
-static int g_kn_cone = 1, g_kn_streams = 0, g_kn_parts = 2;
+static int g_kn_cone = 1, g_kn_streams = 0, g_kn_parts = 2, g_kn_place = 1;
 static pthread_once_t g_kn_once = PTHREAD_ONCE_INIT;
 static pthread_mutex_t g_kn_lock = PTHREAD_MUTEX_INITIALIZER;
 static void decoder_knobs_read(void) {
@@ -387,6 +388,8 @@ static void decoder_knobs_read(void) {
   __atomic_store_n(&g_kn_streams, e ? atoi(e) : 0, __ATOMIC_RELAXED);
   e = getenv("PTD_WINDOW_PARTS");
   __atomic_store_n(&g_kn_parts, e ? atoi(e) : 2, __ATOMIC_RELAXED);
+  e = getenv("PTD_SERVER_PLACE");
+  __atomic_store_n(&g_kn_place, !(e && e[0] == '0'), __ATOMIC_RELAXED);
   pthread_mutex_unlock(&g_kn_lock);
 }
 static int decoder_knob(const int *k) {
@@ -1160,7 +1163,75 @@ int ptd_decode_chunk(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, i
 struct ptd_server {
   int n;
   pt_ctx *ctx;
+  void *ballast[PTDI_PLACE_MAX_BALLAST];   /* idle streams that set where the contexts' go */
 };
+
+/* ---- placement of a server's streams on the hardware queues
+ * HIP binds each new stream to the least-used of its hardware queues (4 by default), counting
+ * every stream the process holds, and a queue runs one kernel at a time.  Which of the contexts'
+ * streams share a queue therefore depends on the streams made before them, which the library can
+ * neither see nor choose, and a queue that carries one stream more than the others bounds a step
+ * of concurrent requests (T = 226 on 8 streams: 1 / 2 / 2 / 3 streams per queue measured ~5 %
+ * slower than 2 / 2 / 2 / 2).  So the servers time it: for 0 .. PTDI_PLACE_MAX_BALLAST idle
+ * streams made first, the contexts' streams are made anew and each runs one bounded
+ * single-workgroup kernel, all at once; they finish in (streams on the busiest queue) x (one
+ * kernel's time).  The fastest arrangement is made again and kept (HIP's choice repeats for the
+ * same sequence of streams).  Only where streams sit changes, not what runs on them. */
+#define PLACE_ITERS 10000
+static int place_make(pt_ctx *ctx, int n, void **ballast, int nb) {
+  for (int i = 0; i < n; i++) {
+    if (ctx[i].g_stream && ptk_stream_destroy(ctx[i].g_stream)) return -1;
+    ctx[i].g_stream = NULL;
+  }
+  for (int k = 0; k < nb; k++)
+    if (ptk_stream_create(&ballast[k])) return -1;
+  for (int i = 0; i < n; i++)
+    if (ptk_stream_create(&ctx[i].g_stream)) return -1;
+  return 0;
+}
+void ptdi_place_release(void **ballast) {
+  for (int k = 0; k < PTDI_PLACE_MAX_BALLAST; k++)
+    if (ballast[k]) {
+      ptk_stream_destroy(ballast[k]);
+      ballast[k] = NULL;
+    }
+}
+static double place_time(pt_ctx *ctx, int n) {
+  double best = 1e30;
+  for (int r = 0; r < 3; r++) {
+    if (ptk_device_sync()) return -1.0;
+    const double t0 = ptdi_now_ms();
+    for (int i = 0; i < n; i++)
+      if (ptk_calib_launch(PLACE_ITERS, ctx[i].g_stream)) return -1.0;
+    if (ptk_device_sync()) return -1.0;
+    const double t = ptdi_now_ms() - t0;
+    if (t < best) best = t;
+  }
+  return best;
+}
+int ptdi_place_streams(pt_ctx *ctx, int n, void **ballast) {
+  if (n < 2 || !decoder_knob(&g_kn_place)) return 0;
+  double best_t = 1e30;
+  int best = 0;
+  for (int nb = 0; nb <= PTDI_PLACE_MAX_BALLAST; nb++) {
+    if (place_make(ctx, n, ballast, nb)) goto fail;
+    const double t = place_time(ctx, n);
+    ptdi_place_release(ballast);
+    if (t < 0.0) goto fail;
+    /* fewer idle streams unless clearly faster */
+    if (t < 0.9 * best_t) {
+      best_t = t;
+      best = nb;
+    }
+  }
+  if (place_make(ctx, n, ballast, best) == 0) return 0;
+fail:
+  PT_LOG("stream placement: %s", ptk_last_error());
+  ptdi_place_release(ballast);
+  for (int i = 0; i < n; i++)
+    if (!ctx[i].g_stream && ptk_stream_create(&ctx[i].g_stream)) return -1;
+  return 0;
+}
 
 ptd_server *ptd_server_create(int nctx, size_t arena_bytes) {
   if (nctx < 1) return NULL;
@@ -1179,6 +1250,10 @@ ptd_server *ptd_server_create(int nctx, size_t arena_bytes) {
     }
   }
   s->n = nctx;
+  if (ptdi_place_streams(s->ctx, nctx, s->ballast)) {
+    ptd_server_destroy(s);
+    return NULL;
+  }
   for (int i = 0; i < nctx; i++) ptdi_aux_prepare(&s->ctx[i]);   /* after every context stream */
   return s;
 }
@@ -1186,6 +1261,7 @@ ptd_server *ptd_server_create(int nctx, size_t arena_bytes) {
 void ptd_server_destroy(ptd_server *s) {
   if (!s) return;
   for (int i = 0; i < s->n; i++) pt_v21_cuda_shutdown(&s->ctx[i]);
+  ptdi_place_release(s->ballast);
   free(s->ctx);
   free(s);
 }

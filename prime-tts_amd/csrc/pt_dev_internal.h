@@ -69,6 +69,13 @@ double ptdi_now_ms(void);
 /* make / release the extra streams a context's windowed decodes split long batched runs over
  * (pt_decoder.c; made on first use when not prepared) */
 void ptdi_aux_prepare(pt_ctx *c);
+/* The contexts' streams remade behind 0 .. PTDI_PLACE_MAX_BALLAST idle streams (kept in ballast,
+ * released by ptdi_place_release), whichever arrangement a timed probe finds spreads them most
+ * evenly over the hardware queues (PTD_SERVER_PLACE=0: left as made).  Call before anything is
+ * queued on them.  0, or -1 when a context is left without a stream. */
+#define PTDI_PLACE_MAX_BALLAST 3
+int ptdi_place_streams(pt_ctx *ctx, int n, void **ballast);
+void ptdi_place_release(void **ballast);
 void ptdi_aux_release(pt_ctx *c);
 /* re-read the PTD_WINDOW_* knobs from the environment (otherwise read once; pt_decoder.c) */
 void ptdi_decoder_knobs_reload(void);

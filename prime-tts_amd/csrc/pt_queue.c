@@ -37,6 +37,7 @@ struct ptd_queue {
   int nw, cap, nthreads;
   size_t arena_bytes;
   pt_ctx *ctx;
+  void *ballast[PTDI_PLACE_MAX_BALLAST];   /* see ptdi_place_streams */
   pthread_t *th;
   qworker_arg *args;
   qjob *slots;
@@ -103,6 +104,7 @@ static void queue_free(struct ptd_queue *q) {
   if (q->ctx)
     for (int i = 0; i < q->nw; i++)
       if (q->ctx[i].use_cuda) pt_v21_cuda_shutdown(&q->ctx[i]);
+  ptdi_place_release(q->ballast);
   pthread_mutex_destroy(&q->mu);
   pthread_cond_destroy(&q->cv_work);
   pthread_cond_destroy(&q->cv_done);
@@ -149,6 +151,10 @@ ptd_queue *ptd_queue_create(const ptd_model *m, int nworkers, size_t arena_bytes
       queue_free(q);
       return NULL;
     }
+  }
+  if (ptdi_place_streams(q->ctx, nworkers, q->ballast)) {
+    queue_free(q);
+    return NULL;
   }
   /* after every worker's stream: a worker's first long-form job then makes no streams */
   for (int i = 0; i < nworkers; i++) ptdi_aux_prepare(&q->ctx[i]);

@@ -20,6 +20,9 @@ const char *ptk_last_error(void);
 int ptk_stream_create(void **s);                   /* non-blocking stream, default priority */
 int ptk_stream_destroy(void *s);
 int ptk_stream_sync(void *s);
+/* one single-workgroup launch of `iters` dependent ALU steps (no memory reads), for timing how
+ * streams share the hardware queues */
+int ptk_calib_launch(int iters, void *s);
 int ptk_stream_query(void *s);                     /* 1 done, 0 busy, -1 error */
 int ptk_malloc(void **p, size_t bytes);
 void ptk_fail_allocs(int skip, int n);   /* tests: after skip more successes, n ptk_malloc calls fail */

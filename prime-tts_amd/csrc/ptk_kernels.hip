@@ -200,6 +200,25 @@ extern "C" int ptk_stream_destroy(void *s) {
   HCHK(hipStreamDestroy((hipStream_t) s));
   return 0;
 }
+// A bounded single-workgroup kernel of dependent ALU work: no memory reads, no waits, one store
+// per lane.  Two launches on one hardware queue run one after the other, on two queues at once,
+// which is how the servers time the queue placement of their streams.
+// (a device symbol the host could read, so the loop and its store are not removed as dead code)
+__device__ float ptk_calib_sink[64];
+__global__ void __launch_bounds__(64) calib_kernel(int iters, float seed) {
+  float v = seed + (float) threadIdx.x;
+  for (int i = 0; i < iters; i++) v = v * 0.999f + 0.5f;
+  ptk_calib_sink[threadIdx.x] = v;
+}
+extern "C" int ptk_calib_launch(int iters, void *s) {
+  if (iters < 1 || iters > (1 << 22)) {
+    set_err("ptk_calib_launch: %d iterations outside [1, 2^22]", iters);
+    return -1;
+  }
+  hipLaunchKernelGGL(calib_kernel, dim3(1), dim3(64), 0, (hipStream_t) s, iters, 1.0f);
+  HCHK(hipGetLastError());
+  return 0;
+}
 extern "C" int ptk_stream_sync(void *s) {
   HCHK(hipStreamSynchronize((hipStream_t) s));
   return 0;

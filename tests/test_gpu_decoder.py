@@ -833,3 +833,41 @@ def test_config5_as_benchmarked(env):
         assert s >= 60.0, f"request {i}"
     for b in dz + dw:
         b.free()
+
+
+def test_server_stream_placement_changes_no_sample(env, knob_env):
+    """ptd_server_create times where its contexts' streams sit on HIP's hardware queues (idle
+    ballast streams made first, a bounded single-workgroup kernel per stream) and keeps the most
+    even arrangement: the T = 226 request on 8 concurrent streams gives the same samples with the
+    placement on and off (PTD_SERVER_PLACE=0), both equal to the batched decode, over repeated
+    servers (the ballast streams are released with each)."""
+    ctx, model, ws, bs = env
+    say("server stream placement: 8 streams of T = 226, placement on / off")
+    lib = ctx.lib
+    T, n = 226, 8
+    zs = [synth.latent(T, 226 + i) for i in range(n)]
+    dz = [dev_of(ctx, z) for z in zs]
+    db = dev_of(ctx, np.concatenate(zs))
+    wb = pkg.DevBuf(n * 256 * T)
+    assert lib.ptd_decode(ctx.ptr, model.ptr, db.ptr, T, n, wb.ptr) == 0
+    batched = wb.download(ctx).reshape(n, -1)
+    arena = int(lib.ptd_decode_arena_bytes(T, 1)) + (16 << 20)
+    try:
+        for place in ("1", "0", "1"):
+            knob_env.setenv("PTD_SERVER_PLACE", place)
+            srv = lib.ptd_server_create(n, arena)
+            assert srv
+            dw = [pkg.DevBuf.of(ctx, np.full(256 * T, np.nan, np.float32)) for _ in range(n)]
+            reqs = (pkg.Request * n)(*[pkg.Request(dz[i].ptr, dw[i].ptr, T, 0, 0) for i in range(n)])
+            wall = C.c_double()
+            try:
+                assert lib.ptd_serve_run(srv, model.ptr, reqs, n, C.byref(wall)) == 0
+            finally:
+                lib.ptd_server_destroy(srv)
+            for i in range(n):
+                assert np.array_equal(dw[i].download(ctx), batched[i]), (place, i)
+            for b in dw:
+                b.free()
+    finally:
+        for b in dz + [db, wb]:
+            b.free()
