@@ -194,7 +194,11 @@ int ptd_decode_chunk(pt_ctx *c, const ptd_model *m, const float *z, int64_t T, i
  * nctx contexts (one stream + arena each, sharing the model's weights), each driven by its own
  * pthread.  ptd_serve_run hands request r to context r % nctx, runs all requests, waits for
  * all of them and returns the wall time in ms (host clock, from the first enqueue to the last
- * stream's completion).  Requests with win > 0 use the windowed path. */
+ * stream's completion).  Requests with win > 0 use the windowed path.  ptd_server_create (and
+ * ptd_queue_create) time where the contexts' streams sit on HIP's hardware queues and keep the
+ * most even arrangement (a few ms of single-workgroup kernels, with the device synchronised
+ * between them: create servers before other work is queued on the device; PTD_SERVER_PLACE=0
+ * skips it). */
 typedef struct ptd_server ptd_server;
 ptd_server *ptd_server_create(int nctx, size_t arena_bytes);
 void ptd_server_destroy(ptd_server *s);
