@@ -19,6 +19,9 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
        python bench.py --decode-loop N [--batch B]   (N config-4 decodes, for a kernel trace)
        python bench.py --streams8-loop N   (N steps of the T = 226 request on 8 concurrent
                                           streams after ~60 ms of the same, for a kernel trace)
+       python bench.py --queue-table KERNEL_TRACE_CSV [--steps N]   (the last N steps of a
+                                          --streams8-loop trace: busy time, kernels in flight,
+                                          kernel time per hardware queue, per kernel)
        python bench.py --layer-table KERNEL_TRACE_CSV [--batch B] [--counters COUNTER_CSV]
                                           (per-launch table of that trace, MFMA utilisation from a
                                           --pmc pass over the same loop)
@@ -267,6 +270,46 @@ def _mfma_util(counter_csv, batch):
         u = [d[i]["SQ_VALU_MFMA_BUSY_CYCLES"] / (d[i]["GRBM_GUI_ACTIVE"] / GRBM_XCDS * SIMDS) for d in dec]
         out.append(100.0 * sum(u) / len(u))
     return out
+
+
+def _kname(r):
+    return r["Kernel_Name"].removeprefix("void ")
+
+
+def queue_table(csv_path, steps, per_step=8 * 19):
+    """Summary of the last `steps` steps of `bench.py --streams8-loop` from a rocprofv3 kernel
+    trace (the last steps x per_step decoder dispatches by start time): busy share of the span,
+    kernels in flight, kernel time per hardware queue (Queue_Id), and per kernel."""
+    import collections
+    import csv
+    import statistics as st
+    rows = [r for r in csv.DictReader(open(csv_path)) if _kname(r).startswith(_DECODER_KERNELS)]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    if len(rows) < steps * per_step:
+        raise SystemExit(f"{len(rows)} decoder dispatches, fewer than {steps} steps of {per_step}")
+    iv = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r) for r in rows[-steps * per_step:]]
+    t0, t1 = min(a for a, _, _ in iv), max(b for _, b, _ in iv)
+    ev = sorted([(a, 1) for a, _, _ in iv] + [(b, -1) for _, b, _ in iv])
+    inflight, k, prev = collections.Counter(), 0, ev[0][0]
+    for t, d in ev:
+        inflight[k] += t - prev
+        k += d
+        prev = t
+    queue, qn, kinds = collections.Counter(), collections.Counter(), collections.defaultdict(list)
+    for a, b, r in iv:
+        queue[r["Queue_Id"]] += (b - a) / 1e3
+        qn[r["Queue_Id"]] += 1
+        kinds[_kname(r).split("(")[0]].append((b - a) / 1e3)
+    span = (t1 - t0) / 1e3
+    tot = sum(b - a for a, b, _ in iv) / 1e3
+    out = [f"{steps} steps: {span / steps:.1f} us per step; kernels running {100 * (1 - inflight[0] / (t1 - t0)):.1f} % "
+           f"of the span; {tot / span:.2f} kernels in flight on average",
+           "in flight: " + ", ".join(f"{n}: {100 * v / (t1 - t0):.1f} %" for n, v in sorted(inflight.items())),
+           "per hardware queue (kernel us per step, launches per step): "
+           + ", ".join(f"{q}: {v / steps:.1f} us, {qn[q] / steps:.1f}" for q, v in sorted(queue.items()))]
+    for name, v in sorted(kinds.items(), key=lambda x: -sum(x[1])):
+        out.append(f"  {name}: {len(v) / steps:.1f} per step, mean {st.mean(v):.2f} us")
+    return "\n".join(out)
 
 
 def layer_table(csv_path, batch, counter_csv=None):
@@ -630,10 +673,14 @@ def main():
     ap.add_argument("--streams8-loop", type=int, default=0)
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--layer-table", metavar="KERNEL_TRACE_CSV")
+    ap.add_argument("--queue-table", metavar="KERNEL_TRACE_CSV")
     ap.add_argument("--counters", metavar="COUNTER_COLLECTION_CSV")
     args = ap.parse_args()
     if args.layer_table:
         print(layer_table(args.layer_table, args.batch, args.counters))
+        return
+    if args.queue_table:
+        print(queue_table(args.queue_table, args.steps))
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "

@@ -218,3 +218,30 @@ def test_warm_keeps_the_stream_fed(monkeypatch):
     kinds = [k if k != "record" else e for k, e in lib.log]
     assert kinds[:5] == ["call", "call", "blocker", t.e0, "call"]
     assert kinds[-2:] == [t.e1, "wait"]
+
+
+def test_queue_table_of_a_multi_stream_trace(tmp_path):
+    """--queue-table: over the last N steps, the share of the span with a kernel running, the
+    kernels in flight and the kernel time per hardware queue, on a synthetic two-queue trace
+    (queue 1: one 10 us kernel after another; queue 2: 30 us kernels, overlapping queue 1)."""
+    bench = _bench()
+    cols = ["Kind", "Queue_Id", "Dispatch_Id", "Kernel_Name", "Start_Timestamp", "End_Timestamp"]
+    rows, did = [], 1
+    for step in range(3):
+        base = step * 100_000
+        for i in range(2):
+            rows.append(["KERNEL_DISPATCH", 1, did, "void conv_mfma_kernel<11>(ConvGroup)",
+                         base + i * 10_000, base + (i + 1) * 10_000])
+            did += 1
+        rows.append(["KERNEL_DISPATCH", 2, did, "tail_kernel<256>(float const*)", base, base + 30_000])
+        did += 1
+    p = tmp_path / "trace.csv"
+    with open(p, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(cols)
+        w.writerows(rows)
+    text = bench.queue_table(str(p), 2, per_step=3)
+    assert "1: 20.0 us, 2.0" in text and "2: 30.0 us, 3" not in text
+    assert "2: 30.0 us, 1.0" in text
+    # steps 1 and 2 span 130 us, kernels run 60 us of it: 2 in flight for 20 us of each step
+    assert "kernels running 46.2 %" in text
